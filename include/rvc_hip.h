@@ -1,0 +1,165 @@
+/*
+ * rvc_hip.h -- C ABI of the MI355X (gfx950) HIP backend for RVC's synthesis
+ * hot path (GeneratorNSF + enc_p + flow).
+ *
+ * The library (librvc_hip.so) is a drop-in for the reference's native engine
+ * at its C boundary: same export names, argument order and meaning, and the
+ * same conventions (engine/src/ffi.zig:1-45):
+ *   - every export returns int32 0 on success, -1 on failure; the message is
+ *     kept in a process-global, mutex-protected buffer read with
+ *     rvc_last_error;
+ *   - rvc_engine_create returns an int64 handle (> 0) or -1;
+ *   - buffer ids are opaque int64 keys; id 0 means "no bias";
+ *   - sizes are float counts, except rvc_mem_alloc / rvc_mem_fill_zero /
+ *     *_bytes which take bytes;
+ *   - f32 scalars (leaky slope, batch layer-norm eps, transpose scale) travel
+ *     as IEEE-754 bit patterns in the low 32 bits of an int64
+ *     (runtime/vulkan_ops.py:255-261);
+ *   - every call on one engine is serialised by that engine's mutex.
+ * Differences from the reference engine: handles are table keys, not raw
+ * pointers (a stale handle is rejected); single ops are enqueued on the
+ * engine's HIP stream and complete before any download returns.
+ *
+ * Everything below the ABI is new MI355X code: fp32 MFMA implicit-GEMM
+ * convolutions, bandwidth-bound fused epilogues, and a device-resident
+ * synthesis session (rvc_synth_*) that has no counterpart in the reference's
+ * ABI (its closest analogue is the BatchRunner record/commit path driven from
+ * runtime/models/vits.py:676-823, 1165-1253, 1660-1842).
+ */
+#ifndef RVC_HIP_H
+#define RVC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- engine */
+/* replaces rvc_engine_create  (engine/src/ffi.zig:50) */
+int64_t rvc_engine_create(void);
+/* replaces rvc_engine_destroy (engine/src/ffi.zig:63) */
+int32_t rvc_engine_destroy(int64_t h);
+
+/* ---------------------------------------------------------------- memory */
+/* replaces rvc_mem_upload       (engine/src/ffi.zig:76): new buffer from n floats */
+int32_t rvc_mem_upload(int64_t h, const float* src, int64_t n, int64_t* out_buf);
+/* replaces rvc_mem_upload_to    (engine/src/ffi.zig:92): overwrite an existing buffer */
+int32_t rvc_mem_upload_to(int64_t h, const float* src, int64_t n, int64_t buf);
+/* replaces rvc_mem_upload_bytes (engine/src/ffi.zig:155): raw bytes (int ids, int64 pitch) */
+int32_t rvc_mem_upload_bytes(int64_t h, const void* src, int64_t nbytes, int64_t* out_buf);
+/* replaces rvc_mem_alloc        (engine/src/ffi.zig:140): uninitialised buffer of nbytes */
+int32_t rvc_mem_alloc(int64_t h, int64_t nbytes, int64_t* out_buf);
+/* replaces rvc_mem_fill_zero    (engine/src/ffi.zig:170): zero the first nbytes */
+int32_t rvc_mem_fill_zero(int64_t h, int64_t buf, int64_t nbytes);
+/* replaces rvc_mem_download     (engine/src/ffi.zig:183): copy n floats to host (waits) */
+int32_t rvc_mem_download(int64_t h, int64_t buf, float* dst, int64_t n);
+/* byte-sized download; no reference counterpart (the reference downloads f32 only) */
+int32_t rvc_mem_download_bytes(int64_t h, int64_t buf, void* dst, int64_t nbytes);
+/* replaces rvc_mem_free         (engine/src/ffi.zig:222) */
+int32_t rvc_mem_free(int64_t h, int64_t buf);
+
+/* ---------------------------------------------------------------- single ops */
+/* replaces rvc_matmul  (engine/src/ffi.zig:233): c[M,N] = a[M,K] @ b[K,N], row-major */
+int32_t rvc_matmul(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* replaces rvc_add / rvc_mul (engine/src/ffi.zig:258, :270): c = a (+|*) b over n floats */
+int32_t rvc_add(int64_t h, int64_t a, int64_t b, int64_t c, int64_t n);
+int32_t rvc_mul(int64_t h, int64_t a, int64_t b, int64_t c, int64_t n);
+/* replaces rvc_relu (engine/src/ffi.zig:282): in place */
+int32_t rvc_relu(int64_t h, int64_t a, int64_t n);
+/* replaces rvc_conv1d (engine/src/ffi.zig:294): x[B,C_in,L], w[C_out,C_in,K], b[C_out] or 0,
+ * out[B,C_out,L_out], L_out = (L+pad_l+pad_r-dil*(K-1)-1)/stride+1; bias added in the kernel */
+int32_t rvc_conv1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                   int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t pad_l, int64_t pad_r,
+                   int64_t dil);
+/* replaces rvc_conv_t1d (engine/src/ffi.zig:336): w[C_in,C_out,K] (PyTorch ConvTranspose1d layout),
+ * L_out = (L-1)*stride - 2*padding + dil*(K-1) + output_padding + 1 */
+int32_t rvc_conv_t1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                     int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t padding,
+                     int64_t output_padding, int64_t dil);
+/* replaces rvc_embed (engine/src/ffi.zig:503): out[n,dim] = table[ids[n],:]; ids are int32,
+ * validated by the caller (negative ids wrap once) */
+int32_t rvc_embed(int64_t h, int64_t ids, int64_t table, int64_t out, int64_t n, int64_t table_rows,
+                  int64_t emb_dim);
+/* replaces rvc_add_inplace / rvc_mul_inplace (engine/src/ffi.zig:522, :534): a (+|*)= b */
+int32_t rvc_add_inplace(int64_t h, int64_t a, int64_t b, int64_t n);
+int32_t rvc_mul_inplace(int64_t h, int64_t a, int64_t b, int64_t n);
+/* replaces rvc_leaky_relu (engine/src/ffi.zig:549): in place, slope as f32 bits */
+int32_t rvc_leaky_relu(int64_t h, int64_t a, int64_t n, int64_t slope);
+/* replaces rvc_copy (engine/src/ffi.zig:563): dst != src */
+int32_t rvc_copy(int64_t h, int64_t dst, int64_t src, int64_t n);
+/* replaces rvc_layernorm (engine/src/ffi.zig:575): row-major [rows, cols], over cols, two-pass */
+int32_t rvc_layernorm(int64_t h, int64_t x, int64_t gamma, int64_t beta, int64_t out, int64_t rows,
+                      int64_t cols, double eps);
+/* replaces rvc_softmax (engine/src/ffi.zig:604): row softmax */
+int32_t rvc_softmax(int64_t h, int64_t x, int64_t out, int64_t rows, int64_t cols);
+
+/* ---------------------------------------------------------------- record / commit */
+/* replaces rvc_batch_begin / add / commit / commit_async / wait / discard
+ * (engine/src/ffi.zig:880-1017).  Supported op codes and parameter layout are
+ * the reference's (engine/src/ffi.zig:888-929): 1 matmul, 2 conv1d, 3 add_inplace,
+ * 4 mul_inplace, 5 conv_t1d, 6 leaky_relu, 7 copy, 8 softmax, 9 layer_norm,
+ * 14 relu, 18 gating, 19 transpose. */
+int32_t rvc_batch_begin(int64_t h);
+int32_t rvc_batch_add(int64_t h, int32_t op, int64_t a, int64_t b, int64_t c, int64_t p0, int64_t p1,
+                      int64_t p2, int64_t p3, int64_t p4, int64_t p5, int64_t p6, int64_t p7, int64_t p8,
+                      int64_t p9, int64_t p10);
+/* replaces rvc_batch_add_copy_seg (engine/src/ffi.zig:753): dst[a_off..+n) = src[b_off..+n) */
+int32_t rvc_batch_add_copy_seg(int64_t h, int64_t a, int64_t b, int64_t n, int64_t a_off, int64_t b_off);
+int32_t rvc_batch_commit(int64_t h);
+int32_t rvc_batch_commit_async(int64_t h);
+int32_t rvc_batch_wait(int64_t h);
+int32_t rvc_batch_discard(int64_t h);
+
+/* ---------------------------------------------------------------- info */
+/* replaces rvc_device_name (engine/src/ffi.zig:1087): needs a live engine */
+int32_t rvc_device_name(char* buf, int64_t buf_size);
+/* replaces rvc_last_error (engine/src/ffi.zig:1110) */
+int32_t rvc_last_error(char* buf, int64_t buf_size);
+
+/* ---------------------------------------------------------------- synthesis session
+ * No counterpart in the reference ABI.  A session owns device-resident,
+ * pre-packed weights of one RVC v2 synthesizer and runs
+ * SynthesizerTrn.infer_controlled (runtime/models/vits.py:2551-2595) or
+ * _GeneratorNSF.forward (runtime/models/vits.py:2133-2231) as one stream of
+ * fused HIP kernels.  Tensors are float32, batch-major; B independent
+ * chunks of P frames each. */
+int64_t rvc_synth_create(int64_t h);
+int32_t rvc_synth_destroy(int64_t s);
+/* Register one checkpoint tensor by its RVC key (e.g. "dec.ups.0.weight_v");
+ * weight-norm pairs are resolved at finalize (runtime/models/vits.py:416-442). */
+int32_t rvc_synth_set_weight(int64_t s, const char* key, const float* data, const int64_t* shape,
+                             int32_t ndim);
+/* Derive the geometry from the registered shapes plus the upsample rates /
+ * kernels and the sample rate (VitsConfig, runtime/models/vits.py:166-268),
+ * pack and upload every weight. */
+int32_t rvc_synth_finalize(int64_t s, int64_t sr, const int64_t* rates, const int64_t* kernels,
+                           int32_t n_ups);
+/* Host in -> host out.  phone [B,P,phone_dim], pitch int64 [B,P], nsff0 [B,P],
+ * sid int64 [B], nz [B,hidden,P], ns [B,P*upp] -> wave [B,P*upp]. */
+int32_t rvc_synth_infer(int64_t s, const float* phone, const int64_t* pitch, const float* nsff0,
+                        const int64_t* sid, const float* nz, const float* ns, int64_t B, int64_t P,
+                        float* wave);
+/* Same with engine buffer ids (inputs already resident; pitch/sid hold int64). */
+int32_t rvc_synth_infer_dev(int64_t s, int64_t phone, int64_t pitch, int64_t nsff0, int64_t sid,
+                            int64_t nz, int64_t ns, int64_t B, int64_t P, int64_t wave);
+/* Decoder only: z [B,hidden,P], f0 [B,P], g [B,gin], ns [B,P*upp] -> wave [B,P*upp]. */
+int32_t rvc_synth_decode(int64_t s, const float* z, const float* f0, const float* g, const float* ns,
+                         int64_t B, int64_t P, float* wave);
+int32_t rvc_synth_decode_dev(int64_t s, int64_t z, int64_t f0, int64_t g, int64_t ns, int64_t B,
+                             int64_t P, int64_t wave);
+/* Copy a named intermediate of the last run to the host (n floats): "enc_in",
+ * "enc_out", "stats", "z_p", "z", "g", "har", "dec_pre", "dec_stage0".."dec_stage3". */
+int32_t rvc_synth_read(int64_t s, const char* name, float* dst, int64_t n);
+/* Keep a copy of each decoder stage output ("dec_stage<i>") for rvc_synth_read. */
+int32_t rvc_synth_set_debug(int64_t s, int32_t keep_stages);
+/* Per-kernel-family timing with HIP events on the session stream.  tag selects
+ * the launches to time (prefix match, e.g. "dec.rb.s1"); "" disables. */
+int32_t rvc_synth_set_timing(int64_t s, const char* tag);
+int32_t rvc_synth_get_timing(int64_t s, double* total_ms, int64_t* launches, double* flops, double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RVC_HIP_H */

@@ -1,0 +1,164 @@
+// Vector-ALU convolutions for the shapes the MFMA kernel does not cover:
+//   * strided conv1d with few input channels (the NSF noise convs,
+//     1 -> C with k = 2*stride; runtime/models/vits.py:1628-1635),
+//   * conv_post (32 -> 1, k7, leaky 0.01 prologue, tanh epilogue;
+//     runtime/models/vits.py:2228-2231),
+//   * the general op-level conv1d (stride > 1) and ConvTranspose1d with
+//     dilation / output_padding (runtime/nn.py:89-135, 293-346).
+// Plus the device-side weight packers for the MFMA kernel.
+#include "internal.h"
+
+namespace rvc {
+namespace {
+
+__device__ __forceinline__ float act_in(float v, int act, float slope) {
+  return (act == ACT_LEAKY && v < 0.f) ? v * slope : v;
+}
+
+__device__ __forceinline__ float act_out(float v, int act, float slope) {
+  if (act == ACT_LEAKY) return v >= 0.f ? v : v * slope;
+  if (act == ACT_TANH) return tanhf(v);
+  if (act == ACT_RELU) return fmaxf(v, 0.f);
+  return v;
+}
+
+constexpr int kTI = 64;            // outputs per workgroup along time
+constexpr int kTCO = 4;            // output channels per workgroup
+constexpr int kWinFloats = 8192;   // LDS window budget (32 KB)
+
+// Workgroup (64 x 4 threads) computes kTI consecutive outputs for kTCO output
+// channels.  The input window of a chunk of channels is staged in LDS so the
+// strided taps read LDS instead of re-fetching global memory.
+__global__ __launch_bounds__(256) void conv1d_direct_kernel(DirectConvArgs a, int win, int cic) {
+  __shared__ float xs[kWinFloats];
+  const int tx = threadIdx.x & 63;
+  const int ty = threadIdx.x >> 6;
+  const int b = blockIdx.z;
+  const int i0 = blockIdx.x * kTI;
+  const int co = blockIdx.y * kTCO + ty;
+  const int i = i0 + tx;
+  const float* xb = a.x + (long long)b * a.xb;
+  const long long tbase = (long long)i0 * a.stride + a.in_off;
+  float acc = 0.f;
+  for (int ci0 = 0; ci0 < a.C_in; ci0 += cic) {
+    const int nci = min(cic, a.C_in - ci0);
+    __syncthreads();
+    for (int e = threadIdx.x; e < nci * win; e += 256) {
+      const int r = e / win;
+      const int j = e - r * win;
+      const long long t = tbase + j;
+      float v = 0.f;
+      if (t >= 0 && t < a.L_in) v = act_in(xb[(long long)(ci0 + r) * a.xc + t], a.in_act, a.in_slope);
+      xs[e] = v;
+    }
+    __syncthreads();
+    if (co < a.C_out && i < a.n_out) {
+      for (int r = 0; r < nci; ++r) {
+        const float* wr = a.w + ((long long)co * a.C_in + ci0 + r) * a.K;
+        const float* xr = xs + r * win + tx * a.stride;
+        for (int k = 0; k < a.K; ++k) acc += wr[k] * xr[k * a.dil];
+      }
+    }
+  }
+  if (co < a.C_out && i < a.n_out) {
+    float v = acc;
+    if (a.bias) v = v + a.bias[co];
+    v = act_out(v, a.out_act, a.out_slope);
+    float* o = a.out + (long long)b * a.ob + (long long)co * a.oc + i;
+    if (a.combine == COMB_ADD) v = *o + v;
+    else if (a.combine == COMB_ADD_DIV) v = (*o + v) / a.div;
+    *o = v;
+  }
+}
+
+// Gather-form ConvTranspose1d: one thread per output element.
+__global__ __launch_bounds__(256) void conv_t1d_direct_kernel(ConvTArgs a) {
+  const long long n = (long long)a.B * a.C_out * a.n_out;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int o = (int)(idx % a.n_out);
+  const int co = (int)((idx / a.n_out) % a.C_out);
+  const int b = (int)(idx / ((long long)a.n_out * a.C_out));
+  const float* xb = a.x + (long long)b * a.xb;
+  float acc = 0.f;
+  for (int k = 0; k < a.K; ++k) {
+    const int num = o + a.padding - k * a.dil;
+    if (num < 0 || num % a.stride != 0) continue;
+    const int t = num / a.stride;
+    if (t >= a.L_in) continue;
+    for (int ci = 0; ci < a.C_in; ++ci)
+      acc += act_in(xb[(long long)ci * a.xc + t], a.in_act, a.in_slope) *
+             a.w[((long long)ci * a.C_out + co) * a.K + k];
+  }
+  float v = acc;
+  if (a.bias) v = v + a.bias[co];
+  float* out = a.out + (long long)b * a.ob + (long long)co * a.oc + o;
+  if (a.combine == COMB_ADD) v = *out + v;
+  *out = v;
+}
+
+__global__ void pack_conv_weight_kernel(const float* w, float* out, int C_out, int C_in, int K) {
+  const long long n = (long long)C_out * C_in * K;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  // idx enumerates the destination [K][C_in][C_out]
+  const int co = (int)(idx % C_out);
+  const int ci = (int)((idx / C_out) % C_in);
+  const int k = (int)(idx / ((long long)C_out * C_in));
+  out[idx] = w[((long long)co * C_in + ci) * K + k];
+}
+
+__global__ void pack_convt_phase_kernel(const float* w, float* out, int C_in, int C_out, int K, int st,
+                                        int r, int J) {
+  const long long n = (long long)J * C_in * C_out;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int co = (int)(idx % C_out);
+  const int ci = (int)((idx / C_out) % C_in);
+  const int jp = (int)(idx / ((long long)C_out * C_in));
+  const int k = r + (J - 1 - jp) * st;
+  out[idx] = w[((long long)ci * C_out + co) * K + k];
+}
+
+unsigned grid1d(long long n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
+  RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.K >= 1 && a.stride >= 1 && a.dil >= 1 && a.B >= 1,
+            "conv1d_direct: invalid shape");
+  if (a.n_out <= 0) return;
+  const int win = (kTI - 1) * a.stride + (a.K - 1) * a.dil + 1;
+  RVC_CHECK(win <= kWinFloats, "conv1d_direct: input window too large for LDS");
+  const int cic = kWinFloats / win;
+  dim3 grid((a.n_out + kTI - 1) / kTI, (a.C_out + kTCO - 1) / kTCO, a.B);
+  hipLaunchKernelGGL(conv1d_direct_kernel, grid, dim3(256), 0, s, a, win, cic);
+  check_launch("conv1d_direct");
+}
+
+void launch_conv_t1d_direct(const ConvTArgs& a, hipStream_t s) {
+  RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.K >= 1 && a.stride >= 1 && a.dil >= 1 && a.B >= 1,
+            "conv_t1d_direct: invalid shape");
+  const long long n = (long long)a.B * a.C_out * a.n_out;
+  if (n <= 0) return;
+  hipLaunchKernelGGL(conv_t1d_direct_kernel, dim3(grid1d(n)), dim3(256), 0, s, a);
+  check_launch("conv_t1d_direct");
+}
+
+void launch_pack_conv_weight(const float* w, float* out, int C_out, int C_in, int K, hipStream_t s) {
+  const long long n = (long long)C_out * C_in * K;
+  if (n == 0) return;
+  hipLaunchKernelGGL(pack_conv_weight_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_out, C_in, K);
+  check_launch("pack_conv_weight");
+}
+
+void launch_pack_convt_phase(const float* w, float* out, int C_in, int C_out, int K, int st, int r,
+                             int J, hipStream_t s) {
+  const long long n = (long long)J * C_in * C_out;
+  if (n == 0) return;
+  hipLaunchKernelGGL(pack_convt_phase_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_in, C_out, K,
+                     st, r, J);
+  check_launch("pack_convt_phase");
+}
+
+}  // namespace rvc

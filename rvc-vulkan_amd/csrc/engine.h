@@ -1,0 +1,52 @@
+// Engine object behind the C ABI: one HIP device, one stream, a registry of
+// device buffers keyed by opaque int64 ids, a growable packing scratch and
+// the pending batch of the record/commit API.
+#pragma once
+
+#include <memory>
+#include <unordered_map>
+
+#include "internal.h"
+
+namespace rvc {
+
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+struct BatchOp {
+  int op;
+  long long a, b, c;
+  long long p[11];
+};
+
+struct Engine {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::unordered_map<long long, DevBuf> bufs;
+  long long next_id = 1;
+  std::string device_name;
+  // scratch for packed weights of op-level calls
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  // record/commit batch
+  std::vector<BatchOp> batch;
+  bool in_flight = false;
+
+  Engine();
+  ~Engine();
+
+  long long add_buffer(void* p, size_t bytes);
+  DevBuf& get(long long id);
+  float* fptr(long long id, long long n_floats, const char* what);  // validates size
+  void* scratch_for(size_t bytes);
+  void sync();
+};
+
+// Handle tables (handles are small sequential integers, never raw pointers,
+// so a stale or forged handle is rejected instead of dereferenced).
+Engine* engine_from_handle(long long h);
+
+}  // namespace rvc

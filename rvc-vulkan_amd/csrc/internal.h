@@ -1,0 +1,189 @@
+// Internal declarations shared by the HIP kernels, the engine and the C ABI.
+//
+// Layout convention inside the engine: every activation tensor is stored
+// channel-major per batch item, [B][C][L] with time contiguous (the PyTorch
+// NCT layout the reference uses for conv1d, runtime/nn.py:8-12).  Strides
+// are passed explicitly so kernels can read channel slices in place.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace rvc {
+
+// ---------------------------------------------------------------- errors
+struct Error : std::runtime_error {
+  explicit Error(const std::string& m) : std::runtime_error(m) {}
+};
+
+void set_last_error(const std::string& msg);
+
+#define RVC_HIP(expr)                                                        \
+  do {                                                                       \
+    hipError_t _e = (expr);                                                  \
+    if (_e != hipSuccess)                                                    \
+      throw ::rvc::Error(std::string(#expr) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+#define RVC_CHECK(cond, msg)                 \
+  do {                                       \
+    if (!(cond)) throw ::rvc::Error(msg);    \
+  } while (0)
+
+void check_launch(const char* what);
+
+// ---------------------------------------------------------------- conv args
+// Activation applied while loading an input tile (prologue) or before the
+// combine step of the epilogue.
+enum Act : int { ACT_NONE = 0, ACT_LEAKY = 1, ACT_TANH = 2, ACT_RELU = 3 };
+
+// How the epilogue value v = act((acc + bias [+ bias2]) [+ res]) lands in out.
+enum Combine : int {
+  COMB_STORE = 0,    // out = v
+  COMB_ADD = 1,      // out = out + v
+  COMB_ADD_DIV = 2,  // out = (out + v) / div
+};
+
+struct ConvArgs {
+  const float* x;       // input [B][C_in stride xc][L_in]
+  long long xb;         // batch stride of x (elements)
+  long long xc;         // channel stride of x
+  const float* w;       // packed weights [K][C_in][C_out]
+  const float* bias;    // [C_out] or null
+  const float* bias2;   // second per-channel addend [B][C_out] (batch stride bias2b) or null
+  long long bias2b;
+  const float* res;     // residual [B][C_out][..] or null (indexed like out)
+  long long rb, rc;
+  float* out;
+  long long ob, oc;
+  int C_in, C_out, L_in, n_out;
+  int K, dil;
+  int in_off;     // input index of output i, tap k: i + in_off + k * dil
+  int out_step;   // output element index = i * out_step + out_off
+  int out_off;
+  int in_act;     float in_slope;
+  int out_act;    float out_slope;
+  int combine;    float div;
+  int B;
+};
+
+// MFMA implicit-GEMM conv1d (stride 1), any K / dilation / padding.
+void launch_conv1d_mfma(const ConvArgs& a, hipStream_t s);
+
+// Direct (vector ALU) conv1d for strided / tiny-channel shapes
+// (noise convs, conv_post): out[b][co][i*out_step+out_off] from
+// x[b][ci][i*stride + in_off + k*dil].
+struct DirectConvArgs {
+  const float* x; long long xb, xc;
+  const float* w;  // PyTorch layout [C_out][C_in][K]
+  const float* bias;
+  float* out; long long ob, oc;
+  int C_in, C_out, L_in, n_out, K, stride, dil, in_off;
+  int in_act; float in_slope;
+  int out_act; float out_slope;
+  int combine; float div;
+  int B;
+};
+void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s);
+
+// ConvTranspose1d in gather form (any stride/padding/output_padding/dilation),
+// weights in PyTorch layout [C_in][C_out][K]; bias added after the taps.
+struct ConvTArgs {
+  const float* x; long long xb, xc;
+  const float* w;
+  const float* bias;
+  float* out; long long ob, oc;
+  int C_in, C_out, L_in, n_out, K, stride, padding, dil;
+  int in_act; float in_slope;
+  int combine;
+  int B;
+};
+void launch_conv_t1d_direct(const ConvTArgs& a, hipStream_t s);
+
+// Polyphase ConvTranspose1d (dilation 1) on the MFMA kernel; w_phases[r]
+// holds the packed weights of phase r (launch_pack_convt_phase).
+void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc, const float* const* w_phases,
+                     const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
+                     int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine);
+
+// Weight packing kernels (device side, used by the op-level ABI).
+// [C_out][C_in][K] -> [K][C_in][C_out]
+void launch_pack_conv_weight(const float* w, float* out, int C_out, int C_in, int K, hipStream_t s);
+// ConvTranspose [C_in][C_out][K], phase r of stride st with J taps:
+// out[j'][ci][co] = w[ci][co][r + (J-1-j')*st]
+void launch_pack_convt_phase(const float* w, float* out, int C_in, int C_out, int K, int st, int r,
+                             int J, hipStream_t s);
+
+// ---------------------------------------------------------------- elementwise
+void launch_leaky(float* a, long long n, float slope, hipStream_t s);
+void launch_relu(float* a, long long n, hipStream_t s);
+void launch_copy(float* dst, const float* src, long long n, hipStream_t s);
+void launch_add_inplace(float* a, const float* b, long long n, hipStream_t s);
+void launch_mul_inplace(float* a, const float* b, long long n, hipStream_t s);
+void launch_add(float* c, const float* a, const float* b, long long n, hipStream_t s);
+void launch_mul(float* c, const float* a, const float* b, long long n, hipStream_t s);
+void launch_fill(float* a, long long n, float v, hipStream_t s);
+// out[i, :] = table[ids[i], :], ids int32 with negative wrap.
+void launch_embed_i32(const int* ids, const float* table, float* out, long long n, int rows, int dim,
+                      hipStream_t s);
+// out[b][p][c] = src[b][c][p] * scale  (per batch, C x P -> P x C)
+void launch_transpose(const float* src, float* out, int B, int C, int P, float scale, hipStream_t s);
+// dst[b][c][t] = src[b][C-1-c][t]
+void launch_flip_channels(const float* src, float* dst, int B, int C, int L, hipStream_t s);
+// x[b][c][t] = lrelu((E[b][c][t] + table[pitch[b][t]][c]) * scale, slope)
+void launch_embed_combine(const float* E, const long long* pitch, const float* table, int rows, float* x,
+                          int B, int C, int P, float scale, float slope, hipStream_t s);
+// acts[b][c][t] = tanh(a[c] + g[c]) * sigmoid(a[H+c] + g[H+c]), a = XI[b], g per batch [2H]
+void launch_wn_gate(const float* XI, long long xib, const float* g, long long gb, float* acts, int B,
+                    int H, int L, hipStream_t s);
+// record/commit op 18: c[i] = tanh(a[i]+g1) * sigmoid(a[i+n]+g2)
+void launch_gating(const float* a, const float* g, float* c, long long n, int lg, int h, long long off,
+                   hipStream_t s);
+// z[b][c][t] = m + exp(logs) * nz * k   with m = st[b][c], logs = st[b][H+c]
+void launch_zp(const float* st, const float* nz, float* z, int B, int H, int L, float k, hipStream_t s);
+// h[b][c][t] += rs[b][c][t] (c<H); skip[b][c][t] (=|+=) rs[b][H+c][t]
+void launch_wn_update(float* h, float* skip, const float* rs, int B, int H, int L, int first,
+                      int last, hipStream_t s);
+// x1[b][c][t] = x1 - m   (x1 strided inside z)
+void launch_sub_inplace_strided(float* x1, long long x1b, const float* m, long long mb, int B,
+                                int C, int L, hipStream_t s);
+// out[b][:] = table[clamp(ids[b])][:]  (int64 ids, negative wrap)
+void launch_gather_rows_i64(const long long* ids, const float* table, float* out, int B, int rows, int dim,
+                            hipStream_t s);
+// out[b][co] = bias[co] + sum_ci W[co][ci] * g[b][ci]   (1x1 conv on a length-1 signal)
+void launch_gemv(const float* W, const float* bias, const float* g, long long gb, float* out,
+                 long long ob, int B, int C_out, int C_in, hipStream_t s);
+
+// ---------------------------------------------------------------- NSF source
+// har[b][p*upp+u] (see kernel docs); acc scratch [B][P]
+void launch_sine_source(const float* f0, const float* ns, float* har, float* acc, int B, int P,
+                        int upp, float sr, float w_lin, float b_lin, hipStream_t s);
+
+// ---------------------------------------------------------------- norms
+// Row-major LayerNorm over the last axis: x[rows][cols].
+void launch_layernorm_rows(const float* x, const float* g, const float* b, float* out, long long rows,
+                           int cols, float eps, hipStream_t s);
+// Channel-major LayerNorm over C for each (b, t): x[b][C][L]
+void launch_layernorm_cols(const float* x, const float* g, const float* b, float* out, int B, int C,
+                           int L, float eps, hipStream_t s);
+void launch_softmax_rows(const float* x, float* out, long long rows, int cols, hipStream_t s);
+
+// ---------------------------------------------------------------- attention
+// Windowed relative-position attention, all heads.
+// qkv[b][3*H*D][P] (q, k, v stacked), emb_k/emb_v [2w+1][D], out[b][H*D][P].
+void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out,
+                             int B, int H, int D, int P, int window, hipStream_t s);
+size_t relpos_attention_max_frames();
+
+// ---------------------------------------------------------------- matmul
+// c[M][N] = a[M][K] @ b[K][N], row-major (op-level rvc_matmul)
+void launch_matmul(const float* a, const float* b, float* c, int M, int K, int N, hipStream_t s);
+
+}  // namespace rvc

@@ -1,0 +1,129 @@
+// LayerNorm and softmax.
+//
+// LayerNorm is the two-pass biased-variance form of the reference numpy
+// path, (x - mean) / sqrt(var + eps) * gamma + beta (runtime/backend.py:
+// 286-295) -- not the single-pass E[x^2]-E[x]^2 of the reference's GLSL
+// (engine/shaders/layernorm.comp:68-70).  Sums accumulate in double.
+// Softmax is exp(x - max) / sum (runtime/backend.py:298-306).
+#include "internal.h"
+
+#pragma clang fp contract(off)
+
+namespace rvc {
+namespace {
+
+__device__ double block_sum_d(double v, double* sh) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) sh[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  const int nw = blockDim.x >> 6;
+  for (int i = 0; i < nw; ++i) t += sh[i];
+  return t;
+}
+
+__device__ float block_max_f(float v, float* sh) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) sh[w] = v;
+  __syncthreads();
+  float t = sh[0];
+  const int nw = blockDim.x >> 6;
+  for (int i = 1; i < nw; ++i) t = fmaxf(t, sh[i]);
+  return t;
+}
+
+// One workgroup per row of a row-major [rows][cols] tensor.
+__global__ __launch_bounds__(256) void layernorm_rows_kernel(const float* x, const float* g, const float* b,
+                                                             float* out, int cols, float eps) {
+  __shared__ double sh[8];
+  const long long row = blockIdx.x;
+  const float* xr = x + row * cols;
+  float* orow = out + row * cols;
+  double s = 0.0;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) s += xr[c];
+  const float mean = (float)(block_sum_d(s, sh) / cols);
+  double v = 0.0;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+    const float d = xr[c] - mean;
+    v += (double)d * d;
+  }
+  const float var = (float)(block_sum_d(v, sh) / cols);
+  const float den = sqrtf(var + eps);
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) orow[c] = (xr[c] - mean) / den * g[c] + b[c];
+}
+
+// Channel-major [B][C][L]: normalise over C for each (b, t); one thread per
+// column, consecutive threads on consecutive t so every channel read is
+// coalesced.
+__global__ __launch_bounds__(256) void layernorm_cols_kernel(const float* x, const float* g, const float* b,
+                                                             float* out, int C, int L, float eps,
+                                                             long long n) {
+  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const long long bi = e / L;
+  const int t = (int)(e - bi * L);
+  const float* xc = x + bi * (long long)C * L + t;
+  float* oc = out + bi * (long long)C * L + t;
+  double s = 0.0;
+  for (int c = 0; c < C; ++c) s += xc[(long long)c * L];
+  const float mean = (float)(s / C);
+  double v = 0.0;
+  for (int c = 0; c < C; ++c) {
+    const float d = xc[(long long)c * L] - mean;
+    v += (double)d * d;
+  }
+  const float var = (float)(v / C);
+  const float den = sqrtf(var + eps);
+  for (int c = 0; c < C; ++c) oc[(long long)c * L] = (xc[(long long)c * L] - mean) / den * g[c] + b[c];
+}
+
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* x, float* out, int cols) {
+  __shared__ float shf[8];
+  __shared__ double shd[8];
+  const long long row = blockIdx.x;
+  const float* xr = x + row * cols;
+  float* orow = out + row * cols;
+  float m = -INFINITY;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) m = fmaxf(m, xr[c]);
+  m = block_max_f(m, shf);
+  double s = 0.0;
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) {
+    const float e = expf(xr[c] - m);
+    orow[c] = e;
+    s += e;
+  }
+  const float sum = (float)block_sum_d(s, shd);
+  for (int c = threadIdx.x; c < cols; c += blockDim.x) orow[c] = orow[c] / sum;
+}
+
+}  // namespace
+
+void launch_layernorm_rows(const float* x, const float* g, const float* b, float* out, long long rows,
+                           int cols, float eps, hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return;
+  RVC_CHECK(rows <= 0x7fffffffLL, "layernorm: too many rows");
+  hipLaunchKernelGGL(layernorm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, g, b, out, cols, eps);
+  check_launch("layernorm_rows");
+}
+
+void launch_layernorm_cols(const float* x, const float* g, const float* b, float* out, int B, int C, int L,
+                           float eps, hipStream_t s) {
+  const long long n = (long long)B * L;
+  if (n <= 0 || C <= 0) return;
+  hipLaunchKernelGGL(layernorm_cols_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, g, b, out,
+                     C, L, eps, n);
+  check_launch("layernorm_cols");
+}
+
+void launch_softmax_rows(const float* x, float* out, long long rows, int cols, hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return;
+  RVC_CHECK(rows <= 0x7fffffffLL, "softmax: too many rows");
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, out, cols);
+  check_launch("softmax_rows");
+}
+
+}  // namespace rvc

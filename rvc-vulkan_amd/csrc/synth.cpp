@@ -1,0 +1,827 @@
+// Device-resident RVC v2 synthesis session (rvc_synth_* exports).
+//
+// Holds the packed weights of one SynthesizerTrnMs*NSFsid and runs
+//   enc_p   runtime/models/vits.py:499-538, 962-1059   (TextEncoder)
+//   flow    runtime/models/vits.py:1086-1145, 1255-1268 (reverse coupling)
+//   dec     runtime/models/vits.py:1468-1501, 2133-2231 (GeneratorNSF)
+// composed as in SynthesizerTrn.infer_controlled (:2551-2595), every op a
+// HIP kernel on the engine stream, intermediates resident in HBM.
+//
+// Fusions relative to the reference's op sequence:
+//   * conv_pre + bias + cond(g) in one conv epilogue (bias2 term);
+//   * noise conv written first, each ConvTranspose phase accumulates on top
+//     (x = ups(lrelu(x)) + noise_conv(har)), the leaky-ReLU applied while the
+//     input tile is staged;
+//   * each ResBlock conv applies leaky-ReLU on load and on store, the second
+//     conv adds the residual, and the last conv of ResBlock j writes the
+//     stage average directly: o1 -> acc, acc + o2 -> acc, (acc + o3) / 3 ->
+//     acc (the numpy order of :2225-2227);
+//   * conv_o / FFN conv_2 add the encoder residual in their epilogue; FFN
+//     conv_1 applies ReLU on store;
+//   * windowed relative-position attention is one kernel (attention.hip).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "../../include/rvc_hip.h"
+#include "engine.h"
+
+namespace rvc {
+
+struct HostT {
+  std::vector<float> data;
+  std::vector<long long> shape;
+};
+
+struct Synth {
+  Engine* eng = nullptr;
+  std::map<std::string, HostT> host;
+  bool ready = false;
+
+  // ---- geometry (VitsConfig, runtime/models/vits.py:166-268) ----
+  int phone_dim = 0, H = 0, F = 0, n_layers = 0, heads = 0, kc = 0, gin = 0, n_spk = 0;
+  int U = 0, n_ups = 0, upp = 0, sr = 0, half = 0, n_flows = 0, pitch_rows = 0;
+  static constexpr int kWnLayers = 3, kWnKernel = 5, kWindow = 10;
+  std::vector<int> rates, kernels, chans, noise_k, noise_s;
+
+  // ---- device weights ----
+  std::vector<void*> owned;
+  float *emb_phone_w = nullptr, *emb_phone_b = nullptr, *emb_pitch = nullptr, *emb_g = nullptr;
+  struct EncL {
+    float *wqkv, *bqkv, *wo, *bo, *ek, *ev, *g1, *b1, *w1, *bf1, *w2, *bf2, *g2, *b2;
+  };
+  std::vector<EncL> enc;
+  float *proj_w = nullptr, *proj_b = nullptr;
+  struct FlowL {
+    float *pre_w, *pre_b, *post_w, *post_b, *cond_w, *cond_b;
+    float *in_w[kWnLayers], *in_b[kWnLayers], *rs_w[kWnLayers], *rs_b[kWnLayers];
+    int rs_out[kWnLayers];
+  };
+  std::vector<FlowL> flows;
+  float *dpre_w = nullptr, *dpre_b = nullptr, *dcond_w = nullptr, *dcond_b = nullptr, *dpost_w = nullptr;
+  float w_lin = 0.f, b_lin = 0.f;
+  struct StageW {
+    std::vector<float*> phases;
+    float* up_b;
+    float *nw, *nb;
+    float* rw[3][2][3];
+    float* rb[3][2][3];
+  };
+  std::vector<StageW> stages;
+
+  // ---- workspace ----
+  std::map<std::string, std::pair<float*, size_t>> ws;
+  bool keep_stages = false;
+  std::string z_name = "z_p";  // workspace buffer holding the last flow output
+
+  // ---- timing ----
+  std::string tag;
+  struct Ev {
+    hipEvent_t a, b;
+    double flops, bytes;
+  };
+  std::vector<Ev> pending;
+  std::vector<hipEvent_t> pool;
+  double t_ms = 0, t_flops = 0, t_bytes = 0;
+  long long t_n = 0;
+
+  ~Synth() {
+    if (eng && eng->stream) (void)hipStreamSynchronize(eng->stream);
+    for (void* p : owned) (void)hipFree(p);
+    for (auto& kv : ws) (void)hipFree(kv.second.first);
+    for (auto& e : pending) pool.push_back(e.a), pool.push_back(e.b);
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+  }
+
+  // -------------------------------------------------------------- weights
+  const HostT& W(const std::string& k) const {
+    auto it = host.find(k);
+    if (it == host.end()) throw Error("missing weight: " + k);
+    return it->second;
+  }
+  bool has(const std::string& k) const { return host.count(k) != 0; }
+
+  std::vector<float> deweight(const std::string& base) const {
+    // W = v * (g / max(||v||, 1e-12)), norm over all dims but 0
+    // (runtime/models/vits.py:416-442)
+    const HostT& v = W(base + ".weight_v");
+    const HostT& g = W(base + ".weight_g");
+    const long long d0 = v.shape[0];
+    const long long per = (long long)v.data.size() / d0;
+    RVC_CHECK((long long)g.data.size() == d0, base + ".weight_g: expected one scale per output channel");
+    std::vector<float> out(v.data.size());
+    for (long long o = 0; o < d0; ++o) {
+      double s = 0;
+      for (long long j = 0; j < per; ++j) s += (double)v.data[o * per + j] * v.data[o * per + j];
+      float norm = (float)std::sqrt(s);
+      norm = std::max(norm, 1e-12f);
+      const float scale = g.data[o] / norm;
+      for (long long j = 0; j < per; ++j) out[o * per + j] = v.data[o * per + j] * scale;
+    }
+    return out;
+  }
+
+  // [C_out][C_in][K] -> [K][C_in][C_out]
+  static std::vector<float> pack(const std::vector<float>& w, long long C_out, long long C_in, long long K) {
+    std::vector<float> o(w.size());
+    for (long long co = 0; co < C_out; ++co)
+      for (long long ci = 0; ci < C_in; ++ci)
+        for (long long k = 0; k < K; ++k) o[(k * C_in + ci) * C_out + co] = w[(co * C_in + ci) * K + k];
+    return o;
+  }
+
+  float* upload(const std::vector<float>& v) {
+    void* p = nullptr;
+    RVC_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 1) * sizeof(float)));
+    owned.push_back(p);
+    if (!v.empty()) RVC_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+    return static_cast<float*>(p);
+  }
+  float* upload_key(const std::string& k) { return upload(W(k).data); }
+
+  float* upload_conv(const std::string& key, long long C_out, long long C_in, long long K, bool wn) {
+    std::vector<float> w;
+    if (wn) {
+      w = deweight(key);
+      const HostT& v = W(key + ".weight_v");
+      check_shape(key + ".weight_v", v.shape, {C_out, C_in, K});
+    } else {
+      const HostT& t = W(key + ".weight");
+      check_shape(key + ".weight", t.shape, {C_out, C_in, K});
+      w = t.data;
+    }
+    return upload(pack(w, C_out, C_in, K));
+  }
+
+  static void check_shape(const std::string& k, const std::vector<long long>& got, std::vector<long long> want) {
+    if (got != want) {
+      std::string g, wv;
+      for (auto x : got) g += std::to_string(x) + ",";
+      for (auto x : want) wv += std::to_string(x) + ",";
+      throw Error("weight " + k + " has shape [" + g + "], expected [" + wv + "]");
+    }
+  }
+
+  float* upload_vec(const std::string& k, long long n) {
+    const HostT& t = W(k);
+    RVC_CHECK((long long)t.data.size() == n, "weight " + k + " must hold " + std::to_string(n) + " values");
+    return upload(t.data);
+  }
+
+  void finalize(int sr_, const std::vector<int>& rates_, const std::vector<int>& kernels_) {
+    RVC_CHECK(!ready, "synth session already finalized");
+    sr = sr_;
+    rates = rates_;
+    kernels = kernels_;
+    n_ups = (int)rates.size();
+    RVC_CHECK(n_ups >= 1 && kernels.size() == rates.size(), "finalize: need matching upsample rates/kernels");
+    const HostT& ep = W("enc_p.emb_phone.weight");
+    RVC_CHECK(ep.shape.size() == 2, "enc_p.emb_phone.weight must be 2-D");
+    H = (int)ep.shape[0];
+    phone_dim = (int)ep.shape[1];
+    F = (int)W("enc_p.encoder.ffn_layers.0.conv_1.weight").shape[0];
+    while (has("enc_p.encoder.attn_layers." + std::to_string(n_layers) + ".conv_q.weight")) ++n_layers;
+    const HostT& erk = W("enc_p.encoder.attn_layers.0.emb_rel_k");
+    RVC_CHECK(erk.shape.size() == 3 && erk.shape[1] == 2 * kWindow + 1, "emb_rel_k must be [1, 21, k_channels]");
+    kc = (int)erk.shape[2];
+    heads = H / kc;
+    RVC_CHECK(heads * kc == H, "hidden must be a multiple of k_channels");
+    const HostT& eg = W("emb_g.weight");
+    n_spk = (int)eg.shape[0];
+    gin = (int)eg.shape[1];
+    U = (int)W("dec.conv_pre.weight").shape[0];
+    pitch_rows = (int)W("enc_p.emb_pitch.weight").shape[0];
+    half = H / 2;
+    upp = 1;
+    for (int r : rates) {
+      RVC_CHECK(r >= 1, "upsample rates must be >= 1");
+      upp *= r;
+    }
+    while (has("flow.flows." + std::to_string(2 * n_flows) + ".pre.weight")) ++n_flows;
+
+    // ---- enc_p ----
+    check_shape("enc_p.emb_phone.weight", ep.shape, {H, phone_dim});
+    emb_phone_w = upload(pack(ep.data, H, phone_dim, 1));
+    emb_phone_b = upload_vec("enc_p.emb_phone.bias", H);
+    check_shape("enc_p.emb_pitch.weight", W("enc_p.emb_pitch.weight").shape, {pitch_rows, H});
+    emb_pitch = upload_key("enc_p.emb_pitch.weight");
+    emb_g = upload_key("emb_g.weight");
+    for (int i = 0; i < n_layers; ++i) {
+      const std::string a = "enc_p.encoder.attn_layers." + std::to_string(i);
+      EncL L{};
+      std::vector<float> qkv, bqkv;
+      for (const char* nm : {"conv_q", "conv_k", "conv_v"}) {
+        const HostT& t = W(a + "." + nm + ".weight");
+        check_shape(a + "." + nm + ".weight", t.shape, {H, H, 1});
+        qkv.insert(qkv.end(), t.data.begin(), t.data.end());
+        const HostT& b = W(a + "." + nm + ".bias");
+        RVC_CHECK((int)b.data.size() == H, a + "." + nm + ".bias size");
+        bqkv.insert(bqkv.end(), b.data.begin(), b.data.end());
+      }
+      L.wqkv = upload(pack(qkv, 3 * H, H, 1));
+      L.bqkv = upload(bqkv);
+      L.wo = upload_conv(a + ".conv_o", H, H, 1, false);
+      L.bo = upload_vec(a + ".conv_o.bias", H);
+      check_shape(a + ".emb_rel_k", W(a + ".emb_rel_k").shape, {1, 2 * kWindow + 1, kc});
+      check_shape(a + ".emb_rel_v", W(a + ".emb_rel_v").shape, {1, 2 * kWindow + 1, kc});
+      L.ek = upload_key(a + ".emb_rel_k");
+      L.ev = upload_key(a + ".emb_rel_v");
+      const std::string n1 = "enc_p.encoder.norm_layers_1." + std::to_string(i);
+      const std::string n2 = "enc_p.encoder.norm_layers_2." + std::to_string(i);
+      L.g1 = upload_vec(n1 + ".gamma", H);
+      L.b1 = upload_vec(n1 + ".beta", H);
+      L.g2 = upload_vec(n2 + ".gamma", H);
+      L.b2 = upload_vec(n2 + ".beta", H);
+      const std::string f = "enc_p.encoder.ffn_layers." + std::to_string(i);
+      L.w1 = upload_conv(f + ".conv_1", F, H, 3, false);
+      L.bf1 = upload_vec(f + ".conv_1.bias", F);
+      L.w2 = upload_conv(f + ".conv_2", H, F, 3, false);
+      L.bf2 = upload_vec(f + ".conv_2.bias", H);
+      enc.push_back(L);
+    }
+    proj_w = upload_conv("enc_p.proj", 2 * H, H, 1, false);
+    proj_b = upload_vec("enc_p.proj.bias", 2 * H);
+
+    // ---- flow ----
+    for (int fi = 0; fi < n_flows; ++fi) {
+      const std::string b = "flow.flows." + std::to_string(2 * fi);
+      FlowL L{};
+      L.pre_w = upload_conv(b + ".pre", H, half, 1, false);
+      L.pre_b = upload_vec(b + ".pre.bias", H);
+      L.post_w = upload_conv(b + ".post", half, H, 1, false);
+      L.post_b = upload_vec(b + ".post.bias", half);
+      const HostT& cv = W(b + ".enc.cond_layer.weight_v");
+      check_shape(b + ".enc.cond_layer.weight_v", cv.shape, {2 * H * kWnLayers, gin, 1});
+      L.cond_w = upload(deweight(b + ".enc.cond_layer"));
+      L.cond_b = upload_vec(b + ".enc.cond_layer.bias", 2 * H * kWnLayers);
+      for (int i = 0; i < kWnLayers; ++i) {
+        const std::string il = b + ".enc.in_layers." + std::to_string(i);
+        L.in_w[i] = upload_conv(il, 2 * H, H, kWnKernel, true);
+        L.in_b[i] = upload_vec(il + ".bias", 2 * H);
+        const std::string rl = b + ".enc.res_skip_layers." + std::to_string(i);
+        L.rs_out[i] = i < kWnLayers - 1 ? 2 * H : H;
+        L.rs_w[i] = upload_conv(rl, L.rs_out[i], H, 1, true);
+        L.rs_b[i] = upload_vec(rl + ".bias", L.rs_out[i]);
+      }
+      flows.push_back(L);
+    }
+
+    // ---- dec ----
+    dpre_w = upload_conv("dec.conv_pre", U, H, 7, false);
+    dpre_b = upload_vec("dec.conv_pre.bias", U);
+    check_shape("dec.cond.weight", W("dec.cond.weight").shape, {U, gin, 1});
+    dcond_w = upload_key("dec.cond.weight");
+    dcond_b = upload_vec("dec.cond.bias", U);
+    RVC_CHECK(W("dec.m_source.l_linear.weight").data.size() == 1 && W("dec.m_source.l_linear.bias").data.size() == 1,
+              "dec.m_source.l_linear must be 1x1");
+    w_lin = W("dec.m_source.l_linear.weight").data[0];
+    b_lin = W("dec.m_source.l_linear.bias").data[0];
+    int c_in = U;
+    for (int i = 0; i < n_ups; ++i) {
+      const std::string up = "dec.ups." + std::to_string(i);
+      const HostT& v = W(up + ".weight_v");
+      RVC_CHECK(v.shape.size() == 3 && v.shape[0] == c_in && v.shape[2] == kernels[i],
+                up + ".weight_v must be [C_in, C_out, K]");
+      const int c = (int)v.shape[1];
+      RVC_CHECK(c == U >> (i + 1), up + ": stage channels must be upsample_initial / 2^(i+1)");
+      chans.push_back(c);
+      StageW S{};
+      const std::vector<float> wt = deweight(up);
+      const int K = kernels[i], st = rates[i];
+      for (int r = 0; r < st; ++r) {
+        const int J = r < K ? (K - r + st - 1) / st : 0;
+        std::vector<float> ph((size_t)J * c_in * c);
+        for (int jp = 0; jp < J; ++jp) {
+          const int k = r + (J - 1 - jp) * st;
+          for (int ci = 0; ci < c_in; ++ci)
+            for (int co = 0; co < c; ++co)
+              ph[((size_t)jp * c_in + ci) * c + co] = wt[((size_t)ci * c + co) * K + k];
+        }
+        S.phases.push_back(upload(ph));
+      }
+      S.up_b = upload_vec(up + ".bias", c);
+      const std::string nc = "dec.noise_convs." + std::to_string(i);
+      const HostT& nw = W(nc + ".weight");
+      RVC_CHECK(nw.shape.size() == 3 && nw.shape[0] == c && nw.shape[1] == 1, nc + ".weight must be [C, 1, k]");
+      const int kn = (int)nw.shape[2];
+      noise_k.push_back(kn);
+      noise_s.push_back(i < n_ups - 1 ? kn / 2 : 1);
+      S.nw = upload_key(nc + ".weight");
+      S.nb = upload_vec(nc + ".bias", c);
+      static const int ks[3] = {3, 7, 11};
+      for (int j = 0; j < 3; ++j)
+        for (int l = 0; l < 2; ++l)
+          for (int g = 0; g < 3; ++g) {
+            const std::string rb = "dec.resblocks." + std::to_string(3 * i + j) + (l == 0 ? ".convs1." : ".convs2.") +
+                                   std::to_string(g);
+            S.rw[j][l][g] = upload_conv(rb, c, c, ks[j], true);
+            S.rb[j][l][g] = upload_vec(rb + ".bias", c);
+          }
+      stages.push_back(S);
+      c_in = c;
+    }
+    check_shape("dec.conv_post.weight", W("dec.conv_post.weight").shape, {1, c_in, 7});
+    dpost_w = upload_key("dec.conv_post.weight");
+    host.clear();
+    ready = true;
+  }
+
+  // -------------------------------------------------------------- workspace
+  float* buf(const std::string& name, size_t n) {
+    auto it = ws.find(name);
+    if (it != ws.end() && it->second.second >= n) return it->second.first;
+    RVC_HIP(hipStreamSynchronize(eng->stream));
+    if (it != ws.end()) {
+      RVC_HIP(hipFree(it->second.first));
+      ws.erase(it);
+    }
+    void* p = nullptr;
+    RVC_HIP(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(float)));
+    ws[name] = {static_cast<float*>(p), n};
+    return static_cast<float*>(p);
+  }
+
+  // stage lengths and the decoder ping-pong capacity for P frames
+  size_t dec_cap(int P) const {
+    size_t cap = (size_t)U * P;
+    long long L = P;
+    for (int i = 0; i < n_ups; ++i) {
+      L *= rates[i];
+      cap = std::max(cap, (size_t)(chans[i] * L));
+    }
+    return cap;
+  }
+
+  // -------------------------------------------------------------- timing
+  bool timed(const char* t) const { return !tag.empty() && std::strncmp(t, tag.c_str(), tag.size()) == 0; }
+  hipEvent_t ev() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e;
+    RVC_HIP(hipEventCreate(&e));
+    return e;
+  }
+  template <class Fn>
+  void run(const char* t, double flops, double bytes, Fn&& fn) {
+    if (!timed(t)) {
+      fn();
+      return;
+    }
+    Ev e{ev(), ev(), flops, bytes};
+    RVC_HIP(hipEventRecord(e.a, eng->stream));
+    fn();
+    RVC_HIP(hipEventRecord(e.b, eng->stream));
+    pending.push_back(e);
+  }
+  void collect_timing() {
+    for (auto& e : pending) {
+      float ms = 0;
+      RVC_HIP(hipEventElapsedTime(&ms, e.a, e.b));
+      t_ms += ms;
+      t_flops += e.flops;
+      t_bytes += e.bytes;
+      ++t_n;
+      pool.push_back(e.a);
+      pool.push_back(e.b);
+    }
+    pending.clear();
+  }
+
+  // -------------------------------------------------------------- conv helpers
+  ConvArgs cargs(const float* x, long long xb, long long xc, const float* w, const float* bias, float* out,
+                 long long ob, long long oc, int B, int C_in, int C_out, int L, int K, int dil, int pad) {
+    ConvArgs a{};
+    a.x = x; a.xb = xb; a.xc = xc;
+    a.w = w; a.bias = bias;
+    a.out = out; a.ob = ob; a.oc = oc;
+    a.C_in = C_in; a.C_out = C_out; a.L_in = L; a.n_out = L;
+    a.K = K; a.dil = dil; a.in_off = -pad; a.out_step = 1; a.out_off = 0;
+    a.combine = COMB_STORE; a.div = 1.f; a.B = B;
+    return a;
+  }
+  void conv(const char* t, const ConvArgs& a) {
+    const double mac = (double)a.B * a.C_out * a.C_in * a.K * a.n_out;
+    double bytes = 4.0 * ((double)a.B * a.C_in * a.L_in + (double)a.B * a.C_out * a.n_out +
+                          (double)a.C_out * a.C_in * a.K);
+    if (a.res) bytes += 4.0 * a.B * a.C_out * a.n_out;
+    if (a.combine != COMB_STORE) bytes += 4.0 * a.B * a.C_out * a.n_out;
+    run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
+  }
+  // 1x1 conv: x [B][C_in][L] -> out [B][C_out][L]
+  ConvArgs c1x1(const float* x, long long xb, const float* w, const float* b, float* out, int B, int C_in, int C_out,
+                int L) {
+    return cargs(x, xb, L, w, b, out, (long long)C_out * L, L, B, C_in, C_out, L, 1, 1, 0);
+  }
+
+  // -------------------------------------------------------------- enc_p + flow
+  // Returns the flow output z [B][H][P] (batch stride H*P) and g [B][gin].
+  const float* enc_flow(const float* phone, const long long* pitch, const long long* sid, const float* nz, int B, int P,
+                        float* g) {
+    hipStream_t s = eng->stream;
+    const long long HP = (long long)H * P;
+    launch_gather_rows_i64(sid, emb_g, g, B, n_spk, gin, s);
+    float* phT = buf("phT", (size_t)B * phone_dim * P);
+    launch_transpose(phone, phT, B, P, phone_dim, 1.0f, s);
+    float* E = buf("encE", (size_t)B * HP);
+    conv("enc.embed", c1x1(phT, (long long)phone_dim * P, emb_phone_w, emb_phone_b, E, B, phone_dim, H, P));
+    float* xin = buf("enc_in", (size_t)B * HP);
+    launch_embed_combine(E, pitch, emb_pitch, pitch_rows, xin, B, H, P, (float)std::sqrt((double)H), 0.1f, s);
+    float* xo = buf("enc_out", (size_t)B * HP);
+    float* qkv = buf("qkv", (size_t)B * 3 * HP);
+    float* att = buf("att", (size_t)B * HP);
+    float* o = buf("enco", (size_t)B * HP);
+    float* f = buf("ffn", (size_t)B * F * P);
+    const float* x = xin;
+    for (int i = 0; i < n_layers; ++i) {
+      const EncL& L = enc[i];
+      conv("enc.qkv", c1x1(x, HP, L.wqkv, L.bqkv, qkv, B, H, 3 * H, P));
+      run("enc.attn", 4.0 * B * heads * (double)P * P * kc, 4.0 * B * 4 * HP,
+          [&] { launch_relpos_attention(qkv, L.ek, L.ev, att, B, heads, kc, P, kWindow, s); });
+      ConvArgs co = c1x1(att, HP, L.wo, L.bo, o, B, H, H, P);
+      co.res = x; co.rb = HP; co.rc = P;
+      conv("enc.o", co);
+      run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g1, L.b1, xo, B, H, P, 1e-5f, s); });
+      ConvArgs c1 = cargs(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
+      c1.out_act = ACT_RELU;
+      conv("enc.ffn", c1);
+      ConvArgs c2 = cargs(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
+      c2.res = xo; c2.rb = HP; c2.rc = P;
+      conv("enc.ffn", c2);
+      run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g2, L.b2, xo, B, H, P, 1e-5f, s); });
+      x = xo;
+    }
+    float* st = buf("stats", (size_t)B * 2 * HP);
+    conv("enc.proj", c1x1(x, HP, proj_w, proj_b, st, B, H, 2 * H, P));
+    float* zp = buf("z_p", (size_t)B * HP);
+    launch_zp(st, nz, zp, B, H, P, 0.66666f, s);
+
+    // flow.reverse: Flip, RC(6), Flip, RC(4), ... RC(0)
+    float* fz[2] = {buf("fz0", (size_t)B * HP), buf("fz1", (size_t)B * HP)};
+    float* h = buf("fh", (size_t)B * HP);
+    float* gv = buf("fgv", (size_t)B * 2 * H * kWnLayers);
+    float* skip = buf("fskip", (size_t)B * HP);
+    float* xi = buf("fxi", (size_t)B * 2 * HP);
+    float* acts = buf("facts", (size_t)B * HP);
+    float* rs = buf("frs", (size_t)B * 2 * HP);
+    float* m = buf("fm", (size_t)B * half * P);
+    const float* src = zp;
+    int k = 0;
+    for (int fi = n_flows - 1; fi >= 0; --fi) {
+      const FlowL& L = flows[fi];
+      float* dst = fz[k];
+      launch_flip_channels(src, dst, B, H, P, s);
+      conv("flow.pre", c1x1(dst, HP, L.pre_w, L.pre_b, h, B, half, H, P));
+      launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s);
+      for (int i = 0; i < kWnLayers; ++i) {
+        conv("flow.in", cargs(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
+                              (kWnKernel - 1) / 2));
+        launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
+        conv("flow.rs", c1x1(acts, HP, L.rs_w[i], L.rs_b[i], rs, B, H, L.rs_out[i], P));
+        launch_wn_update(h, skip, rs, B, H, P, i == 0, i == kWnLayers - 1, s);
+      }
+      conv("flow.post", c1x1(skip, HP, L.post_w, L.post_b, m, B, H, half, P));
+      launch_sub_inplace_strided(dst + (long long)half * P, HP, m, (long long)half * P, B, half, P, s);
+      src = dst;
+      z_name = k == 0 ? "fz0" : "fz1";
+      k ^= 1;
+    }
+    return src;
+  }
+
+  // -------------------------------------------------------------- GeneratorNSF
+  void decode(const float* z, long long zb, const float* g, const float* f0, const float* ns, int B, int P,
+              float* wave) {
+    hipStream_t s = eng->stream;
+    const long long N = (long long)P * upp;
+    float* har = buf("har", (size_t)B * N);
+    float* phase = buf("phase", (size_t)B * P);
+    run("dec.sine", 20.0 * B * N, 4.0 * B * (2.0 * N + P),
+        [&] { launch_sine_source(f0, ns, har, phase, B, P, upp, (float)sr, w_lin, b_lin, s); });
+    float* cv = buf("dec_cond", (size_t)B * U);
+    launch_gemv(dcond_w, dcond_b, g, gin, cv, U, B, U, gin, s);
+    const size_t cap = dec_cap(P);
+    float* X = buf("dX", (size_t)B * cap);
+    float* T = buf("dT", (size_t)B * cap);
+    float* Y = buf("dY", (size_t)B * cap);
+    float* A = buf("dA", (size_t)B * cap);
+    float* pre = buf("dec_pre", (size_t)B * U * P);
+    ConvArgs ca = cargs(z, zb, P, dpre_w, dpre_b, pre, (long long)U * P, P, B, H, U, P, 7, 1, 3);
+    ca.bias2 = cv;
+    ca.bias2b = U;
+    conv("dec.pre", ca);
+    const float* cur = pre;
+    int L = P, c_in = U;
+    static const int ks[3] = {3, 7, 11};
+    static const int ds[3] = {1, 3, 5};
+    char tg[32];
+    for (int i = 0; i < n_ups; ++i) {
+      const int C = chans[i];
+      const int Lo = L * rates[i];
+      const long long CL = (long long)C * Lo;
+      // noise conv: X = noise_conv(har)
+      {
+        DirectConvArgs d{};
+        d.x = har; d.xb = N; d.xc = N;
+        d.w = stages[i].nw; d.bias = stages[i].nb;
+        d.out = X; d.ob = CL; d.oc = Lo;
+        d.C_in = 1; d.C_out = C; d.L_in = (int)N;
+        d.n_out = (int)((N + 2 * (noise_s[i] / 2) - noise_k[i]) / noise_s[i] + 1);
+        RVC_CHECK(d.n_out == Lo, "noise conv length does not match the upsampled length");
+        d.K = noise_k[i]; d.stride = noise_s[i]; d.dil = 1; d.in_off = -(noise_s[i] / 2);
+        d.combine = COMB_STORE; d.div = 1.f; d.B = B;
+        std::snprintf(tg, sizeof tg, "dec.noise.s%d", i);
+        run(tg, 2.0 * B * CL * noise_k[i], 4.0 * B * ((double)N + CL), [&] { launch_conv1d_direct(d, s); });
+      }
+      // ups: X += ConvTranspose1d(lrelu(cur, 0.1)) + bias
+      {
+        const int K = kernels[i], st = rates[i], pad = (K - st) / 2;
+        const int n_out = (L - 1) * st - 2 * pad + K;
+        RVC_CHECK(n_out == Lo, "ConvTranspose output length must equal L * rate");
+        std::vector<const float*> ph(stages[i].phases.begin(), stages[i].phases.end());
+        std::snprintf(tg, sizeof tg, "dec.ups.s%d", i);
+        run(tg, 2.0 * B * (double)c_in * C * K * L, 4.0 * B * ((double)c_in * L + 2.0 * CL) + 4.0 * c_in * C * K,
+            [&] {
+              convt_polyphase(s, cur, (long long)c_in * L, L, ph.data(), stages[i].up_b, X, CL, Lo, B, c_in, C, L, Lo,
+                              K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
+            });
+      }
+      // three ResBlock1 (k = 3, 7, 11), averaged into A
+      std::snprintf(tg, sizeof tg, "dec.rb.s%d", i);
+      for (int j = 0; j < 3; ++j) {
+        const int k = ks[j];
+        const float* src = X;
+        for (int gi = 0; gi < 3; ++gi) {
+          const int d = ds[gi];
+          ConvArgs c1 = cargs(src, CL, Lo, stages[i].rw[j][0][gi], stages[i].rb[j][0][gi], Y, CL, Lo, B, C, C, Lo, k, d,
+                              (k * d - d) / 2);
+          c1.in_act = ACT_LEAKY; c1.in_slope = 0.1f;
+          c1.out_act = ACT_LEAKY; c1.out_slope = 0.1f;
+          conv(tg, c1);
+          float* dst = gi < 2 ? T : A;
+          ConvArgs c2 = cargs(Y, CL, Lo, stages[i].rw[j][1][gi], stages[i].rb[j][1][gi], dst, CL, Lo, B, C, C, Lo, k, 1,
+                              (k - 1) / 2);
+          c2.res = src; c2.rb = CL; c2.rc = Lo;
+          if (gi == 2) {
+            c2.combine = j == 0 ? COMB_STORE : (j == 1 ? COMB_ADD : COMB_ADD_DIV);
+            c2.div = 3.0f;
+          }
+          conv(tg, c2);
+          src = T;
+        }
+      }
+      if (keep_stages) {
+        float* keep = buf("dec_stage" + std::to_string(i), (size_t)B * CL);
+        launch_copy(keep, A, B * CL, s);
+      }
+      cur = A;
+      L = Lo;
+      c_in = C;
+    }
+    DirectConvArgs p{};
+    p.x = cur; p.xb = (long long)c_in * L; p.xc = L;
+    p.w = dpost_w; p.bias = nullptr;
+    p.out = wave; p.ob = L; p.oc = L;
+    p.C_in = c_in; p.C_out = 1; p.L_in = L; p.n_out = L;
+    p.K = 7; p.stride = 1; p.dil = 1; p.in_off = -3;
+    p.in_act = ACT_LEAKY; p.in_slope = 0.01f;
+    p.out_act = ACT_TANH;
+    p.combine = COMB_STORE; p.div = 1.f; p.B = B;
+    run("dec.post", 2.0 * B * c_in * 7.0 * L, 4.0 * B * ((double)c_in * L + L), [&] { launch_conv1d_direct(p, s); });
+  }
+
+  void check_ready() const { RVC_CHECK(ready, "synth session not finalized"); }
+  void check_BP(long long B, long long P) const {
+    RVC_CHECK(B >= 1 && P >= 1 && B <= 4096 && P <= (1 << 22), "invalid batch / frame count");
+    RVC_CHECK((size_t)P <= relpos_attention_max_frames(),
+              "P exceeds the attention kernel's frame limit (" + std::to_string(relpos_attention_max_frames()) + ")");
+  }
+};
+
+namespace {
+std::mutex g_synth_mu;
+std::unordered_map<long long, Synth*> g_synths;
+long long g_next_synth = 1;
+
+Synth* synth_from(long long s) {
+  std::lock_guard<std::mutex> lk(g_synth_mu);
+  auto it = g_synths.find(s);
+  return it == g_synths.end() ? nullptr : it->second;
+}
+}  // namespace
+
+}  // namespace rvc
+
+using namespace rvc;
+
+template <class F>
+static int32_t sguard(int64_t sh, F&& body) {
+  Synth* s = synth_from(sh);
+  if (!s) {
+    set_last_error("invalid synth handle");
+    return -1;
+  }
+  try {
+    std::lock_guard<std::mutex> lk(s->eng->mu);
+    body(*s);
+    return 0;
+  } catch (const std::exception& ex) {
+    set_last_error(ex.what());
+    return -1;
+  }
+}
+
+extern "C" {
+
+int64_t rvc_synth_create(int64_t h) {
+  Engine* e = engine_from_handle(h);
+  if (!e) {
+    set_last_error("invalid engine handle");
+    return -1;
+  }
+  Synth* s = new Synth();
+  s->eng = e;
+  std::lock_guard<std::mutex> lk(g_synth_mu);
+  const long long id = g_next_synth++;
+  g_synths[id] = s;
+  return id;
+}
+
+int32_t rvc_synth_destroy(int64_t sh) {
+  Synth* s = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_synth_mu);
+    auto it = g_synths.find(sh);
+    if (it == g_synths.end()) {
+      set_last_error("invalid synth handle");
+      return -1;
+    }
+    s = it->second;
+    g_synths.erase(it);
+  }
+  {
+    std::lock_guard<std::mutex> lk(s->eng->mu);
+    delete s;
+  }
+  return 0;
+}
+
+int32_t rvc_synth_set_weight(int64_t sh, const char* key, const float* data, const int64_t* shape, int32_t ndim) {
+  return sguard(sh, [&](Synth& s) {
+    RVC_CHECK(!s.ready, "synth session already finalized");
+    RVC_CHECK(key && data && shape && ndim >= 1 && ndim <= 8, "set_weight: invalid arguments");
+    HostT t;
+    long long n = 1;
+    for (int i = 0; i < ndim; ++i) {
+      RVC_CHECK(shape[i] >= 0, "set_weight: negative dimension");
+      t.shape.push_back(shape[i]);
+      n *= shape[i];
+    }
+    t.data.assign(data, data + n);
+    s.host[key] = std::move(t);
+  });
+}
+
+int32_t rvc_synth_finalize(int64_t sh, int64_t sr, const int64_t* rates, const int64_t* kernels, int32_t n_ups) {
+  return sguard(sh, [&](Synth& s) {
+    RVC_CHECK(rates && kernels && n_ups >= 1 && n_ups <= 16 && sr > 0, "finalize: invalid arguments");
+    std::vector<int> r(rates, rates + n_ups), k(kernels, kernels + n_ups);
+    s.finalize((int)sr, r, k);
+  });
+}
+
+int32_t rvc_synth_infer_dev(int64_t sh, int64_t phone, int64_t pitch, int64_t nsff0, int64_t sid, int64_t nz,
+                            int64_t ns, int64_t B, int64_t P, int64_t wave) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    Engine& e = *s.eng;
+    const float* ph = e.fptr(phone, B * P * s.phone_dim, "infer phone");
+    DevBuf& pb = e.get(pitch);
+    RVC_CHECK(pb.bytes >= (size_t)(B * P) * 8, "infer pitch: buffer too small (int64 [B,P])");
+    const float* f0 = e.fptr(nsff0, B * P, "infer nsff0");
+    DevBuf& sb = e.get(sid);
+    RVC_CHECK(sb.bytes >= (size_t)B * 8, "infer sid: buffer too small (int64 [B])");
+    const float* nzp = e.fptr(nz, B * s.H * P, "infer nz");
+    const float* nsp = e.fptr(ns, B * P * s.upp, "infer ns");
+    float* wv = e.fptr(wave, B * P * s.upp, "infer wave");
+    float* g = s.buf("g", (size_t)B * s.gin);
+    const float* z = s.enc_flow(ph, static_cast<const long long*>(pb.ptr), static_cast<const long long*>(sb.ptr), nzp,
+                                (int)B, (int)P, g);
+    s.decode(z, (long long)s.H * P, g, f0, nsp, (int)B, (int)P, wv);
+    e.sync();
+    s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, const float* nsff0, const int64_t* sid,
+                        const float* nz, const float* ns, int64_t B, int64_t P, float* wave) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    RVC_CHECK(phone && pitch && nsff0 && sid && nz && ns && wave, "infer: null pointer");
+    for (long long i = 0; i < B * P; ++i)
+      RVC_CHECK(pitch[i] >= -s.pitch_rows && pitch[i] < s.pitch_rows, "infer: pitch id out of range");
+    for (long long i = 0; i < B; ++i) RVC_CHECK(sid[i] >= -s.n_spk && sid[i] < s.n_spk, "infer: sid out of range");
+    hipStream_t st = s.eng->stream;
+    const long long N = P * s.upp;
+    float* d_ph = s.buf("in_phone", (size_t)(B * P * s.phone_dim));
+    float* d_pitch = s.buf("in_pitch", (size_t)(B * P * 2));
+    float* d_f0 = s.buf("in_f0", (size_t)(B * P));
+    float* d_sid = s.buf("in_sid", (size_t)(B * 2));
+    float* d_nz = s.buf("in_nz", (size_t)(B * s.H * P));
+    float* d_ns = s.buf("in_ns", (size_t)(B * N));
+    float* d_w = s.buf("out_wave", (size_t)(B * N));
+    RVC_HIP(hipMemcpyAsync(d_ph, phone, sizeof(float) * B * P * s.phone_dim, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_pitch, pitch, 8 * B * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_sid, sid, 8 * B, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
+    float* g = s.buf("g", (size_t)B * s.gin);
+    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch),
+                                reinterpret_cast<const long long*>(d_sid), d_nz, (int)B, (int)P, g);
+    s.decode(z, (long long)s.H * P, g, d_f0, d_ns, (int)B, (int)P, d_w);
+    RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
+    RVC_HIP(hipStreamSynchronize(st));
+    s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_decode_dev(int64_t sh, int64_t z, int64_t f0, int64_t g, int64_t ns, int64_t B, int64_t P,
+                             int64_t wave) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    Engine& e = *s.eng;
+    const float* zp = e.fptr(z, B * s.H * P, "decode z");
+    const float* fp = e.fptr(f0, B * P, "decode f0");
+    const float* gp = e.fptr(g, B * s.gin, "decode g");
+    const float* np_ = e.fptr(ns, B * P * s.upp, "decode ns");
+    float* wv = e.fptr(wave, B * P * s.upp, "decode wave");
+    s.decode(zp, (long long)s.H * P, gp, fp, np_, (int)B, (int)P, wv);
+    e.sync();
+    s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_decode(int64_t sh, const float* z, const float* f0, const float* g, const float* ns, int64_t B,
+                         int64_t P, float* wave) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    RVC_CHECK(z && f0 && g && ns && wave, "decode: null pointer");
+    hipStream_t st = s.eng->stream;
+    const long long N = P * s.upp;
+    float* d_z = s.buf("in_z", (size_t)(B * s.H * P));
+    float* d_f0 = s.buf("in_f0", (size_t)(B * P));
+    float* d_g = s.buf("in_g", (size_t)(B * s.gin));
+    float* d_ns = s.buf("in_ns", (size_t)(B * N));
+    float* d_w = s.buf("out_wave", (size_t)(B * N));
+    RVC_HIP(hipMemcpyAsync(d_z, z, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_f0, f0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_g, g, sizeof(float) * B * s.gin, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
+    s.decode(d_z, (long long)s.H * P, d_g, d_f0, d_ns, (int)B, (int)P, d_w);
+    RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
+    RVC_HIP(hipStreamSynchronize(st));
+    s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_read(int64_t sh, const char* name, float* dst, int64_t n) {
+  return sguard(sh, [&](Synth& s) {
+    RVC_CHECK(name && dst && n >= 0, "read: invalid arguments");
+    const std::string nm = std::strcmp(name, "z") == 0 ? s.z_name : std::string(name);
+    auto it = s.ws.find(nm);
+    RVC_CHECK(it != s.ws.end(), std::string("read: no intermediate named ") + name);
+    RVC_CHECK((size_t)n <= it->second.second, std::string("read: ") + name + " holds fewer values");
+    RVC_HIP(hipMemcpyAsync(dst, it->second.first, sizeof(float) * n, hipMemcpyDeviceToHost, s.eng->stream));
+    RVC_HIP(hipStreamSynchronize(s.eng->stream));
+  });
+}
+
+int32_t rvc_synth_set_debug(int64_t sh, int32_t keep_stages) {
+  return sguard(sh, [&](Synth& s) { s.keep_stages = keep_stages != 0; });
+}
+
+int32_t rvc_synth_set_timing(int64_t sh, const char* tag) {
+  return sguard(sh, [&](Synth& s) {
+    s.tag = tag ? tag : "";
+    s.t_ms = s.t_flops = s.t_bytes = 0;
+    s.t_n = 0;
+  });
+}
+
+int32_t rvc_synth_get_timing(int64_t sh, double* total_ms, int64_t* launches, double* flops, double* bytes) {
+  return sguard(sh, [&](Synth& s) {
+    if (total_ms) *total_ms = s.t_ms;
+    if (launches) *launches = s.t_n;
+    if (flops) *flops = s.t_flops;
+    if (bytes) *bytes = s.t_bytes;
+  });
+}
+
+}  // extern "C"
