@@ -1,0 +1,169 @@
+# -*- coding: utf-8 -*-
+"""Benchmark: RVC v2 40k synthesis throughput on one MI355X.
+
+Workload ("config 2"): full synthesizer
+enc_p + flow + GeneratorNSF, fp32, random-init weights, 10 s of 40 kHz audio
+(P = 1000 frames), batch 1.  One step = one ``rvc_synth_infer_dev`` call over
+inputs already resident in HBM (phone [1,1000,768], pitch, nsff0, sid, the
+z_p noise nz and the NSF noise ns), ending with a stream synchronize.
+
+Prints ONE JSON line with the metric, the roofline of the dominant kernel
+(the fp32 MFMA implicit-GEMM ResBlock convolutions, timed with HIP events on
+the session stream over the timed steps) and a CPU baseline (the numpy
+oracle on a bounded 1 s sample of the same workload, on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "rvc-vulkan_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "audio-sec synthesized/sec (10 s @40 kHz, 1 GPU) + HBM GB/s & MFMA util per op"
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+SR = 40000
+P_FRAMES = 1000           # 10 s at 100 frames/s
+CPU_SAMPLE_FRAMES = 100   # 1 s sample for the numpy baseline
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, geom):
+    """The numpy oracle (a restatement of the reference numpy path) on a 1 s
+    sample of the same workload; returns audio-seconds per second."""
+    from oracle import vits_ref
+    from rvc_hip import synthetic as syn
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"),
+                      default=1)
+    except Exception:  # noqa: BLE001
+        threads = 1
+    ref = vits_ref.Synthesizer(w, sr=geom.sr)
+    inp = syn.make_synth_inputs(geom, CPU_SAMPLE_FRAMES, seed=7)
+    ref.infer_controlled(inp["phone"][:, :10], inp["pitch"][:, :10], inp["nsff0"][:, :10], inp["sid"],
+                         inp["nz"][:, :, :10], inp["ns"][:, :10 * geom.upp])  # warm BLAS / allocator
+    t0 = time.perf_counter()
+    ref.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
+    dt = time.perf_counter() - t0
+    audio_s = CPU_SAMPLE_FRAMES / 100.0
+    return {"value": audio_s / dt, "unit": "audio-s/s", "cores": int(threads), "kind": "port",
+            "sample": f"1 s (P={CPU_SAMPLE_FRAMES}) of the config-2 synthesis (same weights, 40k), "
+                      f"numpy oracle, 1 run after a warm-up, {dt:.2f} s wall"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from rvc_hip import _hip, synthetic as syn
+    from rvc_hip.hip_ops import get_context
+    from rvc_hip.synth import HipSynthesizer
+
+    if not _hip.has_so:
+        raise RuntimeError(f"HIP backend missing: {_hip.so_load_error}")
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=0)
+    ctx = get_context()
+    s = HipSynthesizer(w, sr=geom.sr, ctx=ctx)
+    _log(f"bench: device {_hip.device_name()}; weights resident")
+
+    P, B = P_FRAMES, 1
+    inp = syn.make_synth_inputs(geom, P, seed=3)
+    ids = {
+        "phone": ctx.upload(np.ascontiguousarray(inp["phone"], np.float32)),
+        "pitch": ctx.upload(np.ascontiguousarray(inp["pitch"], np.int64)),
+        "f0": ctx.upload(np.ascontiguousarray(inp["nsff0"], np.float32)),
+        "sid": ctx.upload(np.ascontiguousarray(inp["sid"], np.int64)),
+        "nz": ctx.upload(np.ascontiguousarray(inp["nz"], np.float32)),
+        "ns": ctx.upload(np.ascontiguousarray(inp["ns"], np.float32).reshape(-1)),
+    }
+    n_out = P * geom.upp
+    wave_id = ctx.alloc(B * n_out)
+
+    def step():
+        s.infer_dev(ids["phone"], ids["pitch"], ids["f0"], ids["sid"], ids["nz"], ids["ns"], B, P, wave_id)
+
+    for _ in range(args.warmup):
+        step()
+    _log(f"bench: {args.warmup} warm-up steps done")
+
+    # timed region; every step ends with a stream synchronize inside the call
+    s.set_timing("dec.rb")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = time.perf_counter() - t0
+    rb = s.get_timing()
+    s.set_timing("")
+    ms_step = dt * 1e3 / args.steps
+    audio_s = P / 100.0 * B
+    value = audio_s * args.steps / dt
+    _log(f"bench: {args.steps} steps, {ms_step:.3f} ms/step, {value:.1f} audio-s/s")
+
+    # roofline of the dominant kernel family (ResBlock MFMA convs, 216 launches/step)
+    n_launch = max(rb["launches"], 1)
+    avg_s = rb["ms"] / 1e3 / n_launch
+    flops_launch = rb["flops"] / n_launch
+    achieved = flops_launch / avg_s / 1e12 if avg_s > 0 else 0.0
+    roofline = {"kernel": "conv1d_mfma (GeneratorNSF ResBlock convs, all stages)", "bound": "mfma",
+                "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n_launch // args.steps,
+                "share_of_step": round(rb["ms"] / (dt * 1e3), 3)}
+
+    # per-family breakdown (one extra untimed step per family)
+    breakdown = {}
+    for tag in ("dec.rb.s0", "dec.rb.s1", "dec.rb.s2", "dec.rb.s3", "dec.ups", "dec.noise", "dec.post",
+                "dec.sine", "dec.pre", "enc", "flow"):
+        s.set_timing(tag)
+        step()
+        t = s.get_timing()
+        breakdown[tag] = {"ms": round(t["ms"], 4),
+                          "tflops": round(t["flops"] / (t["ms"] / 1e3) / 1e12, 2) if t["ms"] > 0 else None,
+                          "gbs": round(t["bytes"] / (t["ms"] / 1e3) / 1e9, 1) if t["ms"] > 0 else None}
+    s.set_timing("")
+
+    # PCIe-inclusive rate (host numpy in -> host numpy out); reported, never the headline
+    t0 = time.perf_counter()
+    for _ in range(3):
+        s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
+    host_io = audio_s * 3 / (time.perf_counter() - t0)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(w, geom)
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded inputs, random-init weights)",
+        "config": {"workload": "config 2: RVC v2 40k enc_p+flow+GeneratorNSF, 10 s (P=1000), batch 1, fp32",
+                   "frames": P, "batch": B, "sample_rate": SR, "output_samples": n_out},
+        "roofline": roofline, "cpu_baseline": cpu,
+        "host_io_audio_s_per_s": round(host_io, 2), "breakdown": breakdown,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
