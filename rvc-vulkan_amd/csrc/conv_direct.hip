@@ -97,27 +97,27 @@ __global__ __launch_bounds__(256) void conv_t1d_direct_kernel(ConvTArgs a) {
   *out = v;
 }
 
-__global__ void pack_conv_weight_kernel(const float* w, float* out, int C_out, int C_in, int K) {
-  const long long n = (long long)C_out * C_in * K;
+// idx enumerates the destination [K][C_in][ld]; columns co >= C_out are zero
+__global__ void pack_conv_weight_kernel(const float* w, float* out, int C_out, int C_in, int K, int ld) {
+  const long long n = (long long)ld * C_in * K;
   const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= n) return;
-  // idx enumerates the destination [K][C_in][C_out]
-  const int co = (int)(idx % C_out);
-  const int ci = (int)((idx / C_out) % C_in);
-  const int k = (int)(idx / ((long long)C_out * C_in));
-  out[idx] = w[((long long)co * C_in + ci) * K + k];
+  const int co = (int)(idx % ld);
+  const int ci = (int)((idx / ld) % C_in);
+  const int k = (int)(idx / ((long long)ld * C_in));
+  out[idx] = co < C_out ? w[((long long)co * C_in + ci) * K + k] : 0.f;
 }
 
 __global__ void pack_convt_phase_kernel(const float* w, float* out, int C_in, int C_out, int K, int st,
-                                        int r, int J) {
-  const long long n = (long long)J * C_in * C_out;
+                                        int r, int J, int ld) {
+  const long long n = (long long)J * C_in * ld;
   const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= n) return;
-  const int co = (int)(idx % C_out);
-  const int ci = (int)((idx / C_out) % C_in);
-  const int jp = (int)(idx / ((long long)C_out * C_in));
+  const int co = (int)(idx % ld);
+  const int ci = (int)((idx / ld) % C_in);
+  const int jp = (int)(idx / ((long long)ld * C_in));
   const int k = r + (J - 1 - jp) * st;
-  out[idx] = w[((long long)ci * C_out + co) * K + k];
+  out[idx] = co < C_out ? w[((long long)ci * C_out + co) * K + k] : 0.f;
 }
 
 unsigned grid1d(long long n) { return (unsigned)((n + 255) / 256); }
@@ -146,18 +146,20 @@ void launch_conv_t1d_direct(const ConvTArgs& a, hipStream_t s) {
 }
 
 void launch_pack_conv_weight(const float* w, float* out, int C_out, int C_in, int K, hipStream_t s) {
-  const long long n = (long long)C_out * C_in * K;
+  const int ld = packed_ld(C_out);
+  const long long n = (long long)ld * C_in * K;
   if (n == 0) return;
-  hipLaunchKernelGGL(pack_conv_weight_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_out, C_in, K);
+  hipLaunchKernelGGL(pack_conv_weight_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_out, C_in, K, ld);
   check_launch("pack_conv_weight");
 }
 
 void launch_pack_convt_phase(const float* w, float* out, int C_in, int C_out, int K, int st, int r,
                              int J, hipStream_t s) {
-  const long long n = (long long)J * C_in * C_out;
+  const int ld = packed_ld(C_out);
+  const long long n = (long long)J * C_in * ld;
   if (n == 0) return;
   hipLaunchKernelGGL(pack_convt_phase_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_in, C_out, K,
-                     st, r, J);
+                     st, r, J, ld);
   check_launch("pack_convt_phase");
 }
 

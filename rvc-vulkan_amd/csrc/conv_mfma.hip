@@ -2,23 +2,35 @@
 //
 // out[b][co][i] = sum_{ci,k} W[k][ci][co] * act(x[b][ci][i + in_off + k*dil])
 // viewed as a GEMM with M = C_out, N = output positions and a reduction over
-// (ci, k).  One workgroup owns a BM x BN output tile.  For each chunk of BK
-// input channels it stages, in LDS,
-//   * the input window x[ci0:ci0+BK][i0+in_off : i0+in_off+BN+(K-1)*dil]
-//     once -- every tap re-reads the same window at a shift of k*dil, so
-//     the halo is loaded once per chunk instead of K times, and
-//   * the packed weights W[0:K][ci0:ci0+BK][co0:co0+BM].
+// (ci, k).  One workgroup owns a BM x BN output tile.  For each chunk of
+// BK*SK input channels it stages, in LDS,
+//   * the input window x[ci0:ci0+BK*SK][i0+in_off : i0+in_off+BN+(K-1)*dil]
+//     once -- every tap re-reads the same window at a shift of k*dil, so the
+//     halo is loaded once per chunk instead of K times, and
+//   * the packed weights W[0:K][ci0:ci0+BK*SK][co0:co0+BM] (float4 loads).
+// The next chunk's global loads are issued into registers before the MFMAs
+// of the current chunk, so their latency hides behind the matrix work.
+//
 // Each wave computes a WM x WN sub-tile with (WM/32)*(WN/32) 32x32
-// accumulators.  Per MFMA step (two input channels) lane l supplies
-//   A = W[k][ci0+2q+l/32][co_tile + l%32]      (row = co, k-index = ci)
-//   B = xs[2q+l/32][col_tile + l%32 + k*dil]    (k-index = ci, col = i)
+// accumulators.  With SK > 1 the SK waves that share a sub-tile split the
+// staged channels between them (intra-workgroup split-K, for GEMMs with few
+// output columns) and their partial sums are added through LDS at the end.
+// Per MFMA step (two input channels) lane l supplies
+//   A = W[k][c + l/32][co_tile + l%32]         (row = co, k-index = ci)
+//   B = xs[c + l/32][col_tile + l%32 + k*dil]  (k-index = ci, col = i)
 // and the 16 accumulator registers r of lane l hold
 //   row = (r%4) + 4*(l/32) + 8*(r/4), col = l%32.
+//
 // The fused epilogue adds bias (and an optional second per-channel term),
-// an optional residual, applies leaky-ReLU/tanh and combines into the output
-// (store, accumulate, or accumulate-then-divide for the ResBlock average).
-// Output position i is written at i*out_step + out_off, which lets one phase
-// of a polyphase ConvTranspose1d use the same kernel.
+// an optional residual, applies leaky-ReLU / ReLU / tanh and combines into
+// the output (store, accumulate, or accumulate-then-divide).  Output position
+// i is written at i*out_step + out_off, which lets one phase of a polyphase
+// ConvTranspose1d use the same kernel.  A launch may carry up to
+// kMaxConvGroups independent convolutions with the same channel counts
+// (grid z = group x batch): the three ResBlocks of a decoder stage, or all
+// ConvTranspose phases, run as one grid.
+#include <algorithm>
+
 #include "internal.h"
 
 namespace rvc {
@@ -34,34 +46,58 @@ __device__ __forceinline__ float apply_act(float v, int act, float slope) {
   return v;
 }
 
-template <int BM, int BN, int WM, int WN, int BK>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv1d_mfma_kernel(ConvArgs a) {
-  constexpr int NWM = BM / WM;
-  constexpr int NWN = BN / WN;
-  constexpr int NWAVES = NWM * NWN;
-  constexpr int NT = NWAVES * 64;
-  constexpr int TM = WM / 32;
-  constexpr int TN = WN / 32;
-  static_assert(BK % 2 == 0, "BK must be even");
+template <int BM, int BN, int WM, int WN, int BK, int SK>
+struct Cfg {
+  static constexpr int NWM = BM / WM;
+  static constexpr int NWN = BN / WN;
+  static constexpr int NWAVES = NWM * NWN * SK;
+  static constexpr int NT = NWAVES * 64;
+  static constexpr int TM = WM / 32;
+  static constexpr int TN = WN / 32;
+  static constexpr int BKT = BK * SK;
+  static constexpr int XWMAX = BN + kConvHaloMax;
+  static constexpr int XPT = (BKT * XWMAX + NT - 1) / NT;
+  static constexpr int W4ROW = BM / 4;
+  static constexpr int WPT = (kConvTapsMax * BKT * W4ROW + NT - 1) / NT;
+  static size_t lds_bytes(int K, int dil) {
+    const int XW = BN + (K > 0 ? (K - 1) * dil : 0);
+    const size_t stage = sizeof(float) * ((size_t)BKT * XW + (size_t)K * BKT * BM);
+    const size_t red = SK > 1 ? sizeof(float) * (size_t)(SK - 1) * NWM * NWN * TM * TN * 16 * 64 : 0;
+    return stage > red ? stage : red;
+  }
+};
+
+template <int BM, int BN, int WM, int WN, int BK, int SK>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_kernel(ConvLaunch a) {
+  using C = Cfg<BM, BN, WM, WN, BK, SK>;
+  constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = C::BKT;
+  constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
+  static_assert(BK % 2 == 0 && BKT % 4 == 0, "channel chunk must be a multiple of 4");
+
+  const int b = blockIdx.z % a.B;
+  const int gi = blockIdx.z / a.B;
+  const ConvGroup& G = a.g[gi];
+  const int i0 = blockIdx.x * BN;
+  if (i0 >= G.n_out) return;  // uniform for the whole workgroup, before any barrier
+  const int co0 = blockIdx.y * BM;
+  const int K = G.K;
+  const int dil = G.dil;
+  const int XW = BN + (K > 0 ? (K - 1) * dil : 0);
 
   extern __shared__ float smem[];
-  const int K = a.K;
-  const int dil = a.dil;
-  const int XW = BN + (K > 0 ? (K - 1) * dil : 0);
-  float* xs = smem;            // [BK][XW]
-  float* ws = smem + BK * XW;  // [K][BK][BM]
+  float* xs = smem;             // [BKT][XW]
+  float* ws = smem + BKT * XW;  // [K][BKT][BM]   (BKT*XW is a multiple of 4)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave % NWM;
-  const int wn = wave / NWM;
-  const int b = blockIdx.z;
-  const int i0 = blockIdx.x * BN;
-  const int co0 = blockIdx.y * BM;
-  const float* xb = a.x + (long long)b * a.xb;
+  const int wk = wave / (C::NWM * C::NWN);
+  const int wr = wave % (C::NWM * C::NWN);
+  const int wm = wr % C::NWM;
+  const int wn = wr / C::NWM;
   const int half = lane >> 5;
   const int l32 = lane & 31;
+  const float* xb = G.x + (long long)b * a.xb;
 
   floatx16 acc[TM][TN];
 #pragma unroll
@@ -71,83 +107,135 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv1d_mfma_kernel
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.f;
 
-  for (int ci0 = 0; ci0 < a.C_in && K > 0; ci0 += BK) {
-    // ---- stage the input window (prologue activation applied here) ----
-    const int tbase = i0 + a.in_off;
-    for (int r = 0; r < BK; ++r) {
-      const int ci = ci0 + r;
-      const bool cin = ci < a.C_in;
-      const float* xr = xb + (long long)ci * a.xc;
-      for (int j = tid; j < XW; j += NT) {
-        const int t = tbase + j;
-        float v = 0.f;
-        if (cin && t >= 0 && t < a.L_in) {
-          v = xr[t];
-          if (a.in_act == ACT_LEAKY) v = v >= 0.f ? v : v * a.in_slope;
-        }
-        xs[r * XW + j] = v;
-      }
-    }
-    // ---- stage the packed weights ----
-    for (int row = wave; row < K * BK; row += NWAVES) {
-      const int k = row / BK;
-      const int r = row - k * BK;
-      const int ci = ci0 + r;
-      const float* wr = a.w + ((long long)k * a.C_in + ci) * a.C_out + co0;
-      for (int c = lane; c < BM; c += 64) {
-        float v = 0.f;
-        if (ci < a.C_in && co0 + c < a.C_out) v = wr[c];
-        ws[row * BM + c] = v;
-      }
-    }
-    __syncthreads();
+  float xr[XPT];
+  float4 wreg[WPT];
+  const int nx = BKT * XW;
+  const int nw4 = K * BKT * W4ROW;
+  const int tbase = i0 + G.in_off;
 
-    for (int k = 0; k < K; ++k) {
-      const float* wk = ws + k * BK * BM + wm * WM + l32;
-      const float* xk = xs + wn * WN + l32 + k * dil;
+  auto gload = [&](int ci0) {
 #pragma unroll
-      for (int q = 0; q < BK / 2; ++q) {
-        const int r = 2 * q + half;
-        float av[TM], bv[TN];
+    for (int e = 0; e < XPT; ++e) {
+      const int idx = tid + e * NT;
+      const int r = idx / XW;
+      const int j = idx - r * XW;
+      const int ci = ci0 + r;
+      const int t = tbase + j;
+      float v = 0.f;
+      if (idx < nx && ci < a.C_in && t >= 0 && t < a.L_in) v = xb[(long long)ci * a.xc + t];
+      xr[e] = v;
+    }
 #pragma unroll
-        for (int m = 0; m < TM; ++m) av[m] = wk[r * BM + m * 32];
+    for (int e = 0; e < WPT; ++e) {
+      const int idx = tid + e * NT;
+      const int row = idx / W4ROW;
+      const int c4 = idx - row * W4ROW;
+      const int k = row / BKT;
+      const int ci = ci0 + (row - k * BKT);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (idx < nw4 && ci < a.C_in && co0 + 4 * c4 < a.w_ld)
+        v = *reinterpret_cast<const float4*>(G.w + ((long long)k * a.C_in + ci) * a.w_ld + co0 + 4 * c4);
+      wreg[e] = v;
+    }
+  };
+  auto lstore = [&]() {
 #pragma unroll
-        for (int n = 0; n < TN; ++n) bv[n] = xk[r * XW + n * 32];
-#pragma unroll
-        for (int m = 0; m < TM; ++m)
-#pragma unroll
-          for (int n = 0; n < TN; ++n)
-            acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[m], bv[n], acc[m][n], 0, 0, 0);
+    for (int e = 0; e < XPT; ++e) {
+      const int idx = tid + e * NT;
+      if (idx < nx) {
+        float v = xr[e];
+        if (a.in_act == ACT_LEAKY) v = v >= 0.f ? v : v * a.in_slope;
+        xs[idx] = v;
       }
     }
+#pragma unroll
+    for (int e = 0; e < WPT; ++e) {
+      const int idx = tid + e * NT;
+      if (idx < nw4) reinterpret_cast<float4*>(ws)[idx] = wreg[e];
+    }
+  };
+
+  if (K > 0) {
+    const int nchunk = (a.C_in + BKT - 1) / BKT;
+    gload(0);
+    for (int c = 0; c < nchunk; ++c) {
+      lstore();
+      __syncthreads();
+      if (c + 1 < nchunk) gload((c + 1) * BKT);
+      for (int k = 0; k < K; ++k) {
+        const float* wk_ = ws + (k * BKT + wk * BK) * BM + wm * WM + l32;
+        const float* xk = xs + wk * BK * XW + wn * WN + l32 + k * dil;
+#pragma unroll
+        for (int q = 0; q < BK / 2; ++q) {
+          const int r = 2 * q + half;
+          float av[TM], bv[TN];
+#pragma unroll
+          for (int m = 0; m < TM; ++m) av[m] = wk_[r * BM + m * 32];
+#pragma unroll
+          for (int n = 0; n < TN; ++n) bv[n] = xk[r * XW + n * 32];
+#pragma unroll
+          for (int m = 0; m < TM; ++m)
+#pragma unroll
+            for (int n = 0; n < TN; ++n)
+              acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[m], bv[n], acc[m][n], 0, 0, 0);
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  if constexpr (SK > 1) {
+    // partial sums of waves wk > 0 -> LDS, added in wk order by wave wk == 0
+    float* red = smem;
+    constexpr int PER = TM * TN * 16 * 64;
+    if (wk > 0) {
+      float* dst = red + ((wk - 1) * (C::NWM * C::NWN) + wr) * PER;
+#pragma unroll
+      for (int m = 0; m < TM; ++m)
+#pragma unroll
+        for (int n = 0; n < TN; ++n)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dst[((m * TN + n) * 16 + r) * 64 + lane] = acc[m][n][r];
+    }
     __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int s = 1; s < SK; ++s) {
+      const float* src = red + ((s - 1) * (C::NWM * C::NWN) + wr) * PER;
+#pragma unroll
+      for (int m = 0; m < TM; ++m)
+#pragma unroll
+        for (int n = 0; n < TN; ++n)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[m][n][r] += src[((m * TN + n) * 16 + r) * 64 + lane];
+    }
   }
 
   // ---- fused epilogue ----
   const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
-  float* ob = a.out + (long long)b * a.ob;
-  const float* rb = a.res ? a.res + (long long)b * a.rb : nullptr;
+  float* ob = G.out + (long long)b * a.ob;
+  const float* rb = G.res ? G.res + (long long)b * a.rb : nullptr;
 #pragma unroll
   for (int m = 0; m < TM; ++m) {
 #pragma unroll
     for (int n = 0; n < TN; ++n) {
       const int i = i0 + wn * WN + n * 32 + l32;
-      if (i >= a.n_out) continue;
-      const long long t = (long long)i * a.out_step + a.out_off;
+      if (i >= G.n_out) continue;
+      const long long t = (long long)i * G.out_step + G.out_off;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = (r & 3) + 4 * half + 8 * (r >> 2);
         const int co = co0 + wm * WM + m * 32 + row;
         if (co >= a.C_out) continue;
         float v = acc[m][n][r];
-        if (a.bias) v = v + a.bias[co];
+        if (G.bias) v = v + G.bias[co];
         if (bias2) v = v + bias2[co];
         if (rb) v = v + rb[co * a.rc + t];
         v = apply_act(v, a.out_act, a.out_slope);
         float* o = ob + co * a.oc + t;
-        if (a.combine == COMB_ADD) {
+        if (G.combine == COMB_ADD) {
           v = *o + v;
-        } else if (a.combine == COMB_ADD_DIV) {
+        } else if (G.combine == COMB_ADD_DIV) {
           v = (*o + v) / a.div;
         }
         *o = v;
@@ -156,66 +244,64 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv1d_mfma_kernel
   }
 }
 
-template <int BM, int BN, int WM, int WN, int BK>
-void launch_cfg(const ConvArgs& a, hipStream_t s) {
-  constexpr int NT = (BM / WM) * (BN / WN) * 64;
-  const int XW = BN + (a.K > 0 ? (a.K - 1) * a.dil : 0);
-  const size_t lds = sizeof(float) * ((size_t)BK * XW + (size_t)a.K * BK * BM);
-  dim3 grid((a.n_out + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.B);
-  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK>), grid, dim3(NT), lds, s, a);
-  check_launch("conv1d_mfma");
-}
-
-size_t lds_bytes(int BM, int BN, int BK, int K, int dil) {
-  const int XW = BN + (K > 0 ? (K - 1) * dil : 0);
-  return sizeof(float) * ((size_t)BK * XW + (size_t)K * BK * BM);
-}
-
 constexpr size_t kLdsLimit = 65536;
 
-template <int BM, int BN, int WM, int WN>
-bool try_launch(const ConvArgs& a, hipStream_t s) {
-  if (lds_bytes(BM, BN, 16, a.K, a.dil) <= kLdsLimit) {
-    launch_cfg<BM, BN, WM, WN, 16>(a, s);
-    return true;
-  }
-  if (lds_bytes(BM, BN, 8, a.K, a.dil) <= kLdsLimit) {
-    launch_cfg<BM, BN, WM, WN, 8>(a, s);
-    return true;
-  }
-  if (lds_bytes(BM, BN, 2, a.K, a.dil) <= kLdsLimit) {
-    launch_cfg<BM, BN, WM, WN, 2>(a, s);
-    return true;
-  }
-  return false;
+int max_n_out(const ConvLaunch& a) {
+  int n = 0;
+  for (int g = 0; g < a.n_groups; ++g) n = std::max(n, a.g[g].n_out);
+  return n;
 }
 
-long long n_blocks(const ConvArgs& a, int BM, int BN) {
-  return (long long)((a.n_out + BN - 1) / BN) * ((a.C_out + BM - 1) / BM) * a.B;
+template <int BM, int BN, int WM, int WN, int BK, int SK>
+bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
+  using C = Cfg<BM, BN, WM, WN, BK, SK>;
+  size_t lds = 0;
+  for (int g = 0; g < a.n_groups; ++g) lds = std::max(lds, C::lds_bytes(a.g[g].K, a.g[g].dil));
+  if (lds > kLdsLimit) return false;
+  dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B);
+  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK>), grid, dim3(C::NT), lds, s, a);
+  check_launch("conv1d_mfma");
+  return true;
+}
+
+// Workgroups per batch item.  The tile choice deliberately ignores B: the
+// reduction order depends on the tile, so a batched call stays bit-identical
+// to the same chunks run one by one.
+long long n_blocks(const ConvLaunch& a, int BM, int BN) {
+  long long n = 0;
+  for (int g = 0; g < a.n_groups; ++g) n += (long long)((a.g[g].n_out + BN - 1) / BN) * ((a.C_out + BM - 1) / BM);
+  return n;
 }
 
 }  // namespace
 
-void launch_conv1d_mfma(const ConvArgs& a, hipStream_t s) {
-  RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.n_out >= 0 && a.K >= 0 && a.dil >= 1 && a.B >= 1,
+bool conv1d_mfma_supported(int K, int dil) {
+  return K >= 0 && K <= kConvTapsMax && dil >= 1 && (K > 0 ? (K - 1) * dil : 0) <= kConvHaloMax;
+}
+
+void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
+  RVC_CHECK(a.n_groups >= 1 && a.n_groups <= kMaxConvGroups, "conv1d_mfma: bad group count");
+  RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.B >= 1 && a.w_ld >= a.C_out && a.w_ld % 4 == 0,
             "conv1d_mfma: invalid shape");
-  if (a.n_out == 0) return;
-  // Tile choice: the widest co tile that divides C_out, shrunk while the grid
-  // would leave CUs idle (256 CUs; aim for >= 2 workgroups per CU).
-  const long long want = 512;
-  bool ok = false;
-  if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= want) {
-    ok = try_launch<128, 128, 64, 64>(a, s);
-  } else if (a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want) {
-    ok = try_launch<64, 128, 32, 64>(a, s);
-  } else if (a.C_out % 64 == 0) {
-    ok = try_launch<64, 64, 32, 32>(a, s);
-  } else if (a.C_out <= 32 && n_blocks(a, 32, 256) >= want) {
-    ok = try_launch<32, 256, 32, 64>(a, s);
-  } else {
-    ok = try_launch<32, 128, 32, 32>(a, s);
+  for (int g = 0; g < a.n_groups; ++g) {
+    RVC_CHECK(a.g[g].n_out >= 0 && conv1d_mfma_supported(a.g[g].K, a.g[g].dil),
+              "conv1d_mfma: taps / dilation outside the MFMA path");
+    RVC_CHECK((reinterpret_cast<uintptr_t>(a.g[g].w) & 15) == 0, "conv1d_mfma: weights must be 16-byte aligned");
   }
-  RVC_CHECK(ok, "conv1d_mfma: kernel window does not fit in LDS (K*dil too large)");
+  if (max_n_out(a) == 0) return;
+  // Tile choice: widest co tile that divides C_out while the grid still
+  // gives every CU work (256 CUs); few output columns -> split-K waves.
+  const long long want = 384;
+  bool ok = false;
+  if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= want) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
+  if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)
+    ok = launch_cfg<64, 128, 32, 64, 16, 1>(a, s) || launch_cfg<64, 128, 32, 64, 8, 1>(a, s);
+  if (!ok && a.C_out <= 32 && n_blocks(a, 32, 256) >= want)
+    ok = launch_cfg<32, 256, 32, 64, 16, 1>(a, s) || launch_cfg<32, 256, 32, 64, 8, 1>(a, s);
+  if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 64) >= want)
+    ok = launch_cfg<64, 64, 32, 32, 16, 1>(a, s) || launch_cfg<64, 64, 32, 32, 8, 1>(a, s);
+  if (!ok) ok = launch_cfg<32, 64, 32, 32, 8, 4>(a, s) || launch_cfg<32, 64, 32, 32, 4, 4>(a, s);
+  RVC_CHECK(ok, "conv1d_mfma: no tile configuration fits the LDS budget");
 }
 
 }  // namespace rvc

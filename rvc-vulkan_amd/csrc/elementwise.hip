@@ -50,6 +50,9 @@ __global__ void mul_kernel(float* c, const float* a, const float* b, long long n
 __global__ void fill_kernel(float* a, long long n, float v) {
   GRID_STRIDE(i, n) a[i] = v;
 }
+__global__ void avg3_kernel(float* o, const float* a, const float* b, const float* c, long long n) {
+  GRID_STRIDE(i, n) o[i] = ((a[i] + b[i]) + c[i]) / 3.0f;
+}
 
 // ids are validated by the host; the clamp only keeps a bad device-resident
 // id from reading outside the table.
@@ -299,6 +302,11 @@ void launch_fill(float* a, long long n, float v, hipStream_t s) {
   if (n <= 0) return;
   hipLaunchKernelGGL(fill_kernel, dim3(capped_grid(n)), dim3(256), 0, s, a, n, v);
   check_launch("fill");
+}
+void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(avg3_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, b, c, n);
+  check_launch("avg3");
 }
 void launch_embed_i32(const int* ids, const float* table, float* out, long long n, int rows, int dim,
                       hipStream_t s) {

@@ -103,6 +103,21 @@ float bits_to_f32(long long v) {
   return f;
 }
 
+// A one-group MFMA launch over x [B][C_in][L] -> out [B][C_out][n_out].
+ConvLaunch one_conv(const float* x, long long C_in, long long L, const float* packed, const float* bias, float* out,
+                    long long C_out, long long n_out, long long B, long long K, long long dil, long long pad_l) {
+  ConvLaunch a{};
+  a.n_groups = 1;
+  ConvGroup& g = a.g[0];
+  g.x = x; g.w = packed; g.bias = bias; g.res = nullptr; g.out = out;
+  g.K = (int)K; g.dil = (int)dil; g.in_off = (int)-pad_l; g.out_step = 1; g.out_off = 0;
+  g.n_out = (int)n_out; g.combine = COMB_STORE;
+  a.xb = C_in * L; a.xc = L; a.ob = C_out * n_out; a.oc = n_out;
+  a.C_in = (int)C_in; a.C_out = (int)C_out; a.w_ld = packed_ld((int)C_out); a.L_in = (int)L; a.B = (int)B;
+  a.div = 1.f;
+  return a;
+}
+
 void op_conv1d(Engine& e, long long x, long long w, long long b, long long out, long long B, long long C_in,
                long long L, long long C_out, long long K, long long stride, long long pad_l, long long pad_r,
                long long dil) {
@@ -115,17 +130,10 @@ void op_conv1d(Engine& e, long long x, long long w, long long b, long long out, 
   const float* wp = e.fptr(w, C_out * C_in * K, "conv1d w");
   const float* bp = b ? e.fptr(b, C_out, "conv1d bias") : nullptr;
   float* op = e.fptr(out, B * C_out * n_out, "conv1d out");
-  if (stride == 1) {
-    float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * C_out * C_in * K));
+  if (stride == 1 && conv1d_mfma_supported((int)K, (int)dil)) {
+    float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * packed_ld((int)C_out) * C_in * K));
     launch_pack_conv_weight(wp, packed, (int)C_out, (int)C_in, (int)K, e.stream);
-    ConvArgs a{};
-    a.x = xp; a.xb = C_in * L; a.xc = L;
-    a.w = packed; a.bias = bp;
-    a.out = op; a.ob = C_out * n_out; a.oc = n_out;
-    a.C_in = (int)C_in; a.C_out = (int)C_out; a.L_in = (int)L; a.n_out = (int)n_out;
-    a.K = (int)K; a.dil = (int)dil; a.in_off = (int)-pad_l; a.out_step = 1; a.out_off = 0;
-    a.combine = COMB_STORE; a.div = 1.f; a.B = (int)B;
-    launch_conv1d_mfma(a, e.stream);
+    launch_conv1d_mfma(one_conv(xp, C_in, L, packed, bp, op, C_out, n_out, B, K, dil, pad_l), e.stream);
   } else {
     DirectConvArgs a{};
     a.x = xp; a.xb = C_in * L; a.xc = L;
@@ -143,13 +151,18 @@ void op_conv1d(Engine& e, long long x, long long w, long long b, long long out, 
 // Polyphase ConvTranspose1d on the MFMA kernel (dilation 1): output o with
 // (o + padding) = m*stride + r only sees taps k = r + j*stride of input
 // m - j, so phase r is a stride-1 conv over m with J_r taps whose outputs land
-// at o = m*stride + r - padding.  Shared by the op-level export and the
-// synthesis session.  `w_phases[r]` must hold the packed phase weights.
+// at o = m*stride + r - padding.  All phases go into one grouped launch.
+// Shared by the op-level export and the synthesis session.
 void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc, const float* const* w_phases,
                      const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
                      int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine) {
+  RVC_CHECK(stride >= 1 && stride <= kMaxConvGroups, "conv_transpose1d: stride exceeds the grouped launch");
+  ConvLaunch a{};
+  a.xb = xb; a.xc = xc; a.ob = ob; a.oc = oc;
+  a.C_in = C_in; a.C_out = C_out; a.w_ld = packed_ld(C_out); a.L_in = L; a.B = B;
+  a.in_act = in_act; a.in_slope = in_slope; a.div = 1.f;
   for (int r = 0; r < stride; ++r) {
-    const int J = r < K ? (K - r + stride - 1) / stride : 0;
+    const int J = convt_phase_taps(K, stride, r);
     // m range with 0 <= m*stride + r - padding < n_out
     const int lo = padding - r;
     const int m0 = lo <= 0 ? 0 : (lo + stride - 1) / stride;
@@ -157,17 +170,13 @@ void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc,
     if (hi < 0) continue;
     const int m1 = hi / stride;
     if (m1 < m0) continue;
-    ConvArgs a{};
-    a.x = x; a.xb = xb; a.xc = xc;
-    a.w = w_phases[r]; a.bias = bias;
-    a.out = out; a.ob = ob; a.oc = oc;
-    a.C_in = C_in; a.C_out = C_out; a.L_in = L; a.n_out = m1 - m0 + 1;
-    a.K = J; a.dil = 1; a.in_off = m0 - (J > 0 ? J - 1 : 0);
-    a.out_step = stride; a.out_off = m0 * stride + r - padding;
-    a.in_act = in_act; a.in_slope = in_slope;
-    a.combine = combine; a.div = 1.f; a.B = B;
-    launch_conv1d_mfma(a, st);
+    ConvGroup& g = a.g[a.n_groups++];
+    g.x = x; g.w = w_phases[r]; g.bias = bias; g.res = nullptr; g.out = out;
+    g.K = J; g.dil = 1; g.in_off = m0 - (J > 0 ? J - 1 : 0);
+    g.out_step = stride; g.out_off = m0 * stride + r - padding;
+    g.n_out = m1 - m0 + 1; g.combine = combine;
   }
+  if (a.n_groups > 0) launch_conv1d_mfma(a, st);
 }
 
 namespace {
@@ -184,16 +193,17 @@ void op_conv_t1d(Engine& e, long long x, long long w, long long b, long long out
   const float* wp = e.fptr(w, C_in * C_out * K, "conv_t1d w");
   const float* bp = b ? e.fptr(b, C_out, "conv_t1d bias") : nullptr;
   float* op = e.fptr(out, B * C_out * n_out, "conv_t1d out");
-  if (dil == 1) {
-    // packed phases back to back in the scratch
-    float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * (C_in * C_out * (K + stride))));
+  const int ld = packed_ld((int)C_out);
+  if (dil == 1 && stride <= kMaxConvGroups && (K + stride - 1) / stride <= kConvTapsMax) {
+    // packed phases back to back in the scratch (16-byte aligned: ld % 4 == 0)
+    float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * C_in * ld * (K + stride)));
     std::vector<const float*> phases(stride);
     long long off = 0;
     for (int r = 0; r < stride; ++r) {
-      const int J = r < K ? (int)((K - r + stride - 1) / stride) : 0;
+      const int J = convt_phase_taps((int)K, (int)stride, r);
       launch_pack_convt_phase(wp, packed + off, (int)C_in, (int)C_out, (int)K, (int)stride, r, J, e.stream);
       phases[r] = packed + off;
-      off += (long long)J * C_in * C_out;
+      off += (long long)J * C_in * ld;
     }
     convt_polyphase(e.stream, xp, C_in * L, L, phases.data(), bp, op, C_out * n_out, n_out, (int)B, (int)C_in,
                     (int)C_out, (int)L, (int)n_out, (int)K, (int)stride, (int)padding, ACT_NONE, 0.f, COMB_STORE);
@@ -214,18 +224,11 @@ void op_matmul(Engine& e, long long a, long long b, long long c, long long M, lo
   const float* ap = e.fptr(a, M * K, "matmul a");
   const float* bp = e.fptr(b, K * N, "matmul b");
   float* cp = e.fptr(c, M * N, "matmul c");
-  // c[M][N] = a[M][K] b[K][N] as a 1x1 conv: channels = K, time = N,
-  // weights packed [1][K][M] = a^T.
-  float* at = static_cast<float*>(e.scratch_for(sizeof(float) * M * K));
-  launch_transpose(ap, at, 1, (int)M, (int)K, 1.0f, e.stream);
-  ConvArgs g{};
-  g.x = bp; g.xb = K * N; g.xc = N;
-  g.w = at;
-  g.out = cp; g.ob = M * N; g.oc = N;
-  g.C_in = (int)K; g.C_out = (int)M; g.L_in = (int)N; g.n_out = (int)N;
-  g.K = 1; g.dil = 1; g.in_off = 0; g.out_step = 1; g.out_off = 0;
-  g.combine = COMB_STORE; g.div = 1.f; g.B = 1;
-  launch_conv1d_mfma(g, e.stream);
+  // c[M][N] = a[M][K] b[K][N] as a 1x1 conv: channels = K, time = N; the
+  // packed weights are a^T (a seen as a [M][K][1] conv weight).
+  float* at = static_cast<float*>(e.scratch_for(sizeof(float) * packed_ld((int)M) * K));
+  launch_pack_conv_weight(ap, at, (int)M, (int)K, 1, e.stream);
+  launch_conv1d_mfma(one_conv(bp, K, N, at, nullptr, cp, M, N, 1, 1, 1, 0), e.stream);
 }
 
 void op_layernorm(Engine& e, long long x, long long g, long long b, long long out, long long rows, long long cols,

@@ -51,31 +51,49 @@ enum Combine : int {
   COMB_ADD_DIV = 2,  // out = (out + v) / div
 };
 
-struct ConvArgs {
-  const float* x;       // input [B][C_in stride xc][L_in]
-  long long xb;         // batch stride of x (elements)
-  long long xc;         // channel stride of x
-  const float* w;       // packed weights [K][C_in][C_out]
-  const float* bias;    // [C_out] or null
-  const float* bias2;   // second per-channel addend [B][C_out] (batch stride bias2b) or null
-  long long bias2b;
-  const float* res;     // residual [B][C_out][..] or null (indexed like out)
-  long long rb, rc;
+// MFMA fast path bounds: taps per conv and the input halo (K-1)*dil.
+constexpr int kConvTapsMax = 11;
+constexpr int kConvHaloMax = 64;
+constexpr int kMaxConvGroups = 12;
+
+// One convolution of a grouped MFMA launch (fields that differ per group).
+struct ConvGroup {
+  const float* x;     // input [B][C_in (stride xc)][L_in]
+  const float* w;     // packed weights [K][C_in][w_ld], 16-byte aligned
+  const float* bias;  // [C_out] or null
+  const float* res;   // residual, indexed like out, or null
   float* out;
-  long long ob, oc;
-  int C_in, C_out, L_in, n_out;
   int K, dil;
-  int in_off;     // input index of output i, tap k: i + in_off + k * dil
-  int out_step;   // output element index = i * out_step + out_off
+  int in_off;         // input index of output i, tap k: i + in_off + k * dil
+  int out_step;       // output element index = i * out_step + out_off
   int out_off;
-  int in_act;     float in_slope;
-  int out_act;    float out_slope;
-  int combine;    float div;
-  int B;
+  int n_out;
+  int combine;
 };
 
-// MFMA implicit-GEMM conv1d (stride 1), any K / dilation / padding.
-void launch_conv1d_mfma(const ConvArgs& a, hipStream_t s);
+// A launch of up to kMaxConvGroups convolutions with the same channel
+// counts, strides and activations (grid z = group * B + batch).
+struct ConvLaunch {
+  ConvGroup g[kMaxConvGroups];
+  int n_groups;
+  long long xb, xc;   // batch / channel stride of x
+  long long ob, oc;   // of out
+  long long rb, rc;   // of res
+  const float* bias2; // second per-channel addend [B][C_out] or null
+  long long bias2b;
+  int C_in, C_out, w_ld, L_in, B;
+  int in_act;  float in_slope;
+  int out_act; float out_slope;
+  float div;
+};
+
+// MFMA implicit-GEMM conv1d (stride 1), K <= kConvTapsMax and
+// (K-1)*dil <= kConvHaloMax.
+bool conv1d_mfma_supported(int K, int dil);
+void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s);
+
+// packed-weight leading dimension for C_out output channels
+inline int packed_ld(int c_out) { return (c_out + 3) / 4 * 4; }
 
 // Direct (vector ALU) conv1d for strided / tiny-channel shapes
 // (noise convs, conv_post): out[b][co][i*out_step+out_off] from
@@ -107,17 +125,20 @@ struct ConvTArgs {
 };
 void launch_conv_t1d_direct(const ConvTArgs& a, hipStream_t s);
 
-// Polyphase ConvTranspose1d (dilation 1) on the MFMA kernel; w_phases[r]
-// holds the packed weights of phase r (launch_pack_convt_phase).
+// Polyphase ConvTranspose1d (dilation 1) on the MFMA kernel, all phases in
+// one grouped launch; w_phases[r] holds the packed weights of phase r
+// (launch_pack_convt_phase), ld packed_ld(C_out).  stride <= kMaxConvGroups.
 void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc, const float* const* w_phases,
                      const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
                      int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine);
+// taps of phase r of a stride-st ConvTranspose with K taps
+inline int convt_phase_taps(int K, int st, int r) { return r < K ? (K - r + st - 1) / st : 0; }
 
 // Weight packing kernels (device side, used by the op-level ABI).
-// [C_out][C_in][K] -> [K][C_in][C_out]
+// [C_out][C_in][K] -> [K][C_in][packed_ld(C_out)] (pad columns zero)
 void launch_pack_conv_weight(const float* w, float* out, int C_out, int C_in, int K, hipStream_t s);
 // ConvTranspose [C_in][C_out][K], phase r of stride st with J taps:
-// out[j'][ci][co] = w[ci][co][r + (J-1-j')*st]
+// out[j'][ci][co] = w[ci][co][r + (J-1-j')*st], ld packed_ld(C_out)
 void launch_pack_convt_phase(const float* w, float* out, int C_in, int C_out, int K, int st, int r,
                              int J, hipStream_t s);
 
@@ -130,6 +151,8 @@ void launch_mul_inplace(float* a, const float* b, long long n, hipStream_t s);
 void launch_add(float* c, const float* a, const float* b, long long n, hipStream_t s);
 void launch_mul(float* c, const float* a, const float* b, long long n, hipStream_t s);
 void launch_fill(float* a, long long n, float v, hipStream_t s);
+// out = ((a + b) + c) / 3   (the ResBlock average, runtime/models/vits.py:2225-2227)
+void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s);
 // out[i, :] = table[ids[i], :], ids int32 with negative wrap.
 void launch_embed_i32(const int* ids, const float* table, float* out, long long n, int rows, int dim,
                       hipStream_t s);

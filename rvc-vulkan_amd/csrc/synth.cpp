@@ -13,9 +13,9 @@
 //     (x = ups(lrelu(x)) + noise_conv(har)), the leaky-ReLU applied while the
 //     input tile is staged;
 //   * each ResBlock conv applies leaky-ReLU on load and on store, the second
-//     conv adds the residual, and the last conv of ResBlock j writes the
-//     stage average directly: o1 -> acc, acc + o2 -> acc, (acc + o3) / 3 ->
-//     acc (the numpy order of :2225-2227);
+//     conv adds the residual; the three ResBlocks of a stage share every
+//     conv launch (one grid per dilation group) and are averaged as
+//     ((o_3 + o_7) + o_11) / 3 (the numpy order of :2225-2227);
 //   * conv_o / FFN conv_2 add the encoder residual in their epilogue; FFN
 //     conv_1 applies ReLU on store;
 //   * windowed relative-position attention is one kernel (attention.hip).
@@ -121,12 +121,13 @@ struct Synth {
     return out;
   }
 
-  // [C_out][C_in][K] -> [K][C_in][C_out]
+  // [C_out][C_in][K] -> [K][C_in][packed_ld(C_out)], pad columns zero
   static std::vector<float> pack(const std::vector<float>& w, long long C_out, long long C_in, long long K) {
-    std::vector<float> o(w.size());
+    const long long ld = packed_ld((int)C_out);
+    std::vector<float> o((size_t)(K * C_in * ld), 0.f);
     for (long long co = 0; co < C_out; ++co)
       for (long long ci = 0; ci < C_in; ++ci)
-        for (long long k = 0; k < K; ++k) o[(k * C_in + ci) * C_out + co] = w[(co * C_in + ci) * K + k];
+        for (long long k = 0; k < K; ++k) o[(k * C_in + ci) * ld + co] = w[(co * C_in + ci) * K + k];
     return o;
   }
 
@@ -288,14 +289,16 @@ struct Synth {
       StageW S{};
       const std::vector<float> wt = deweight(up);
       const int K = kernels[i], st = rates[i];
+      RVC_CHECK(st <= kMaxConvGroups && (K + st - 1) / st <= kConvTapsMax, up + ": stride / taps unsupported");
+      const int ld = packed_ld(c);
       for (int r = 0; r < st; ++r) {
-        const int J = r < K ? (K - r + st - 1) / st : 0;
-        std::vector<float> ph((size_t)J * c_in * c);
+        const int J = convt_phase_taps(K, st, r);
+        std::vector<float> ph((size_t)J * c_in * ld, 0.f);
         for (int jp = 0; jp < J; ++jp) {
           const int k = r + (J - 1 - jp) * st;
           for (int ci = 0; ci < c_in; ++ci)
             for (int co = 0; co < c; ++co)
-              ph[((size_t)jp * c_in + ci) * c + co] = wt[((size_t)ci * c + co) * K + k];
+              ph[((size_t)jp * c_in + ci) * ld + co] = wt[((size_t)ci * c + co) * K + k];
         }
         S.phases.push_back(upload(ph));
       }
@@ -391,28 +394,34 @@ struct Synth {
   }
 
   // -------------------------------------------------------------- conv helpers
-  ConvArgs cargs(const float* x, long long xb, long long xc, const float* w, const float* bias, float* out,
-                 long long ob, long long oc, int B, int C_in, int C_out, int L, int K, int dil, int pad) {
-    ConvArgs a{};
-    a.x = x; a.xb = xb; a.xc = xc;
-    a.w = w; a.bias = bias;
-    a.out = out; a.ob = ob; a.oc = oc;
-    a.C_in = C_in; a.C_out = C_out; a.L_in = L; a.n_out = L;
-    a.K = K; a.dil = dil; a.in_off = -pad; a.out_step = 1; a.out_off = 0;
-    a.combine = COMB_STORE; a.div = 1.f; a.B = B;
+  // One stride-1 conv x [B][C_in][L] -> out [B][C_out][L] ("same" length).
+  ConvLaunch cargs(const float* x, long long xb, long long xc, const float* w, const float* bias, float* out,
+                   long long ob, long long oc, int B, int C_in, int C_out, int L, int K, int dil, int pad) {
+    ConvLaunch a{};
+    a.n_groups = 1;
+    ConvGroup& g = a.g[0];
+    g.x = x; g.w = w; g.bias = bias; g.res = nullptr; g.out = out;
+    g.K = K; g.dil = dil; g.in_off = -pad; g.out_step = 1; g.out_off = 0; g.n_out = L; g.combine = COMB_STORE;
+    a.xb = xb; a.xc = xc; a.ob = ob; a.oc = oc;
+    a.C_in = C_in; a.C_out = C_out; a.w_ld = packed_ld(C_out); a.L_in = L; a.B = B;
+    a.div = 1.f;
     return a;
   }
-  void conv(const char* t, const ConvArgs& a) {
-    const double mac = (double)a.B * a.C_out * a.C_in * a.K * a.n_out;
-    double bytes = 4.0 * ((double)a.B * a.C_in * a.L_in + (double)a.B * a.C_out * a.n_out +
-                          (double)a.C_out * a.C_in * a.K);
-    if (a.res) bytes += 4.0 * a.B * a.C_out * a.n_out;
-    if (a.combine != COMB_STORE) bytes += 4.0 * a.B * a.C_out * a.n_out;
+  void conv(const char* t, const ConvLaunch& a) {
+    double mac = 0, bytes = 4.0 * (double)a.B * a.C_in * a.L_in;
+    for (int i = 0; i < a.n_groups; ++i) {
+      const ConvGroup& g = a.g[i];
+      const double outs = (double)a.B * a.C_out * g.n_out;
+      mac += outs * a.C_in * g.K;
+      bytes += 4.0 * (outs + (double)a.C_out * a.C_in * g.K);
+      if (g.res) bytes += 4.0 * outs;
+      if (g.combine != COMB_STORE) bytes += 4.0 * outs;
+    }
     run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
   }
   // 1x1 conv: x [B][C_in][L] -> out [B][C_out][L]
-  ConvArgs c1x1(const float* x, long long xb, const float* w, const float* b, float* out, int B, int C_in, int C_out,
-                int L) {
+  ConvLaunch c1x1(const float* x, long long xb, const float* w, const float* b, float* out, int B, int C_in,
+                  int C_out, int L) {
     return cargs(x, xb, L, w, b, out, (long long)C_out * L, L, B, C_in, C_out, L, 1, 1, 0);
   }
 
@@ -440,15 +449,15 @@ struct Synth {
       conv("enc.qkv", c1x1(x, HP, L.wqkv, L.bqkv, qkv, B, H, 3 * H, P));
       run("enc.attn", 4.0 * B * heads * (double)P * P * kc, 4.0 * B * 4 * HP,
           [&] { launch_relpos_attention(qkv, L.ek, L.ev, att, B, heads, kc, P, kWindow, s); });
-      ConvArgs co = c1x1(att, HP, L.wo, L.bo, o, B, H, H, P);
-      co.res = x; co.rb = HP; co.rc = P;
+      ConvLaunch co = c1x1(att, HP, L.wo, L.bo, o, B, H, H, P);
+      co.g[0].res = x; co.rb = HP; co.rc = P;
       conv("enc.o", co);
       run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g1, L.b1, xo, B, H, P, 1e-5f, s); });
-      ConvArgs c1 = cargs(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
+      ConvLaunch c1 = cargs(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
       c1.out_act = ACT_RELU;
       conv("enc.ffn", c1);
-      ConvArgs c2 = cargs(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
-      c2.res = xo; c2.rb = HP; c2.rc = P;
+      ConvLaunch c2 = cargs(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
+      c2.g[0].res = xo; c2.rb = HP; c2.rc = P;
       conv("enc.ffn", c2);
       run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g2, L.b2, xo, B, H, P, 1e-5f, s); });
       x = xo;
@@ -504,11 +513,15 @@ struct Synth {
     launch_gemv(dcond_w, dcond_b, g, gin, cv, U, B, U, gin, s);
     const size_t cap = dec_cap(P);
     float* X = buf("dX", (size_t)B * cap);
-    float* T = buf("dT", (size_t)B * cap);
-    float* Y = buf("dY", (size_t)B * cap);
     float* A = buf("dA", (size_t)B * cap);
+    float* T[3];
+    float* Y[3];
+    for (int j = 0; j < 3; ++j) {
+      T[j] = buf("dT" + std::to_string(j), (size_t)B * cap);
+      Y[j] = buf("dY" + std::to_string(j), (size_t)B * cap);
+    }
     float* pre = buf("dec_pre", (size_t)B * U * P);
-    ConvArgs ca = cargs(z, zb, P, dpre_w, dpre_b, pre, (long long)U * P, P, B, H, U, P, 7, 1, 3);
+    ConvLaunch ca = cargs(z, zb, P, dpre_w, dpre_b, pre, (long long)U * P, P, B, H, U, P, 7, 1, 3);
     ca.bias2 = cv;
     ca.bias2b = U;
     conv("dec.pre", ca);
@@ -548,30 +561,38 @@ struct Synth {
                               K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
             });
       }
-      // three ResBlock1 (k = 3, 7, 11), averaged into A
+      // three ResBlock1 (k = 3, 7, 11) run side by side: each conv launch
+      // carries the same dilation group of all three blocks (k = 11 first, so
+      // its longer workgroups are dispatched first); block j keeps its state
+      // in T[j]; then A = ((o_3 + o_7) + o_11) / 3.
       std::snprintf(tg, sizeof tg, "dec.rb.s%d", i);
-      for (int j = 0; j < 3; ++j) {
-        const int k = ks[j];
-        const float* src = X;
-        for (int gi = 0; gi < 3; ++gi) {
-          const int d = ds[gi];
-          ConvArgs c1 = cargs(src, CL, Lo, stages[i].rw[j][0][gi], stages[i].rb[j][0][gi], Y, CL, Lo, B, C, C, Lo, k, d,
-                              (k * d - d) / 2);
-          c1.in_act = ACT_LEAKY; c1.in_slope = 0.1f;
-          c1.out_act = ACT_LEAKY; c1.out_slope = 0.1f;
-          conv(tg, c1);
-          float* dst = gi < 2 ? T : A;
-          ConvArgs c2 = cargs(Y, CL, Lo, stages[i].rw[j][1][gi], stages[i].rb[j][1][gi], dst, CL, Lo, B, C, C, Lo, k, 1,
-                              (k - 1) / 2);
-          c2.res = src; c2.rb = CL; c2.rc = Lo;
-          if (gi == 2) {
-            c2.combine = j == 0 ? COMB_STORE : (j == 1 ? COMB_ADD : COMB_ADD_DIV);
-            c2.div = 3.0f;
-          }
-          conv(tg, c2);
-          src = T;
+      for (int gi = 0; gi < 3; ++gi) {
+        const int d = ds[gi];
+        ConvLaunch c1 = cargs(nullptr, CL, Lo, nullptr, nullptr, nullptr, CL, Lo, B, C, C, Lo, 1, 1, 0);
+        ConvLaunch c2 = c1;
+        c1.n_groups = c2.n_groups = 3;
+        c1.in_act = ACT_LEAKY; c1.in_slope = 0.1f;
+        c1.out_act = ACT_LEAKY; c1.out_slope = 0.1f;
+        c2.rb = CL; c2.rc = Lo;
+        for (int z = 0; z < 3; ++z) {
+          const int j = 2 - z;
+          const int k = ks[j];
+          const float* src = gi == 0 ? X : T[j];
+          ConvGroup& g1 = c1.g[z];
+          g1.x = src; g1.w = stages[i].rw[j][0][gi]; g1.bias = stages[i].rb[j][0][gi]; g1.res = nullptr;
+          g1.out = Y[j]; g1.K = k; g1.dil = d; g1.in_off = -((k * d - d) / 2);
+          ConvGroup& g2 = c2.g[z];
+          g2.x = Y[j]; g2.w = stages[i].rw[j][1][gi]; g2.bias = stages[i].rb[j][1][gi]; g2.res = src;
+          g2.out = T[j]; g2.K = k; g2.dil = 1; g2.in_off = -((k - 1) / 2);
+          g1.out_step = g2.out_step = 1;
+          g1.out_off = g2.out_off = 0;
+          g1.n_out = g2.n_out = Lo;
+          g1.combine = g2.combine = COMB_STORE;
         }
+        conv(tg, c1);
+        conv(tg, c2);
       }
+      run("dec.avg", 0.0, 16.0 * B * CL, [&] { launch_avg3(A, T[0], T[1], T[2], B * CL, s); });
       if (keep_stages) {
         float* keep = buf("dec_stage" + std::to_string(i), (size_t)B * CL);
         launch_copy(keep, A, B * CL, s);
