@@ -136,7 +136,7 @@ def main():
 
     # per-family breakdown (one extra untimed step per family)
     breakdown = {}
-    for tag in ("dec.rb.s0", "dec.rb.s1", "dec.rb.s2", "dec.rb.s3", "dec.ups", "dec.noise", "dec.post",
+    for tag in ("dec.rb.s0", "dec.rb.s1", "dec.rb.s2", "dec.rb.s3", "dec.avg", "dec.ups", "dec.noise", "dec.post",
                 "dec.sine", "dec.pre", "enc", "flow"):
         s.set_timing(tag)
         step()

@@ -1,7 +1,7 @@
 // Windowed relative-position self-attention of enc_p (VITS T5-style, window
-// w = 10), fused: scores, band terms, softmax and the weighted sums run in
-// one kernel without materialising the [H,P,P] or [H,P,2P-1] tensors the
-// numpy path builds (runtime/models/vits.py:994-1016).
+// w = 10) as fused fp32 MFMA kernels, flash style: no [H,P,P] score tensor
+// and none of the [H,P,2P-1] rel/abs tensors the numpy path builds
+// (runtime/models/vits.py:994-1016).
 //
 //   qs_t       = q_t / sqrt(D)
 //   score[t,s] = qs_t . k_s  +  [|s-t| <= w] qs_t . emb_k[s-t+w]
@@ -9,114 +9,347 @@
 //   out_t      = sum_s p[t,s] v_s  +  sum_{|s-t|<=w} p[t,s] emb_v[s-t+w]
 //
 // emb_rel is zero outside the window after _get_relative_embeddings
-// (runtime/models/vits.py:448-462), so only the 2w+1 band diagonals carry
-// the relative terms.  One workgroup handles TQ query rows of one head; the
-// full score rows live in LDS.
+// (runtime/models/vits.py:448-462), so only the 2w+1 band diagonals carry the
+// relative terms.
+//
+// A workgroup owns 32 queries of one head and one slice of the keys (the key
+// axis is split over KS workgroups so short sequences still fill the GPU);
+// its 4 waves take every 4th 32-key tile of the slice and keep their own
+// running max / sum / output (online softmax), merged through LDS.  With
+// KS > 1 the slices' partial (max, sum, output) go to a scratch buffer and a
+// second kernel merges them.
+//
+// Per key tile a wave computes S^T = K_tile^T Q with v_mfma_f32_32x32x2_f32
+// (rows = keys in registers, columns = queries in lanes), so the per-query
+// softmax statistics are a reduction over the lane's own registers plus one
+// swap with the other half-wave, and the probabilities already sit in the
+// B-operand layout of O^T += V P^T: MFMA step r pairs key rows (r%4)+8*(r/4)
+// and (r%4)+4+8*(r/4), exactly the rows accumulator register r holds in the
+// two half-waves.  The band terms: R^T[r][t] = emb_k[r] . qs_t is one extra
+// MFMA tile added to the in-band scores; the in-band probabilities are
+// collected per wave ([2w+1][32], rescaled with the running max) and
+// contracted with emb_v by MFMA after the key loop.
+#include <algorithm>
+
 #include "internal.h"
 
 namespace rvc {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
 namespace {
 
-constexpr int TQ = 8;
-constexpr int DMAX = 128;
-constexpr size_t kLdsMax = 65536;
+constexpr int AWAVES = 4;
+constexpr int kMaxWindow = 15;  // 2w+1 <= 31 band rows fit one 32-row tile
 
+__device__ __forceinline__ int acc_row(int r, int half) { return (r & 3) + 4 * half + 8 * (r >> 2); }
+
+template <int DT>
+struct AttnLds {
+  static constexpr int ROWS = DT * 32;
+  static constexpr int VSTRIDE = 33;
+  static constexpr int Q = ROWS * 32;                  // qs[d][t]
+  static constexpr int V = AWAVES * ROWS * VSTRIDE;    // per-wave V tiles
+  static constexpr int MERGE = (AWAVES - 1) * (DT * 16 * 64 + 2 * 32);
+  static constexpr int R = 32 * 32;                    // R^T[r][t]
+  static constexpr int PB = AWAVES * 32 * 32;          // per-wave band probabilities [r][t]
+  static constexpr int VM = V > MERGE ? V : MERGE;
+  static constexpr int TOTAL = Q + VM + R + PB;
+};
+
+template <int DT>
 __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv, const float* emb_k,
-                                                               const float* emb_v, float* out, int H, int D,
-                                                               int P, int window) {
+                                                               const float* emb_v, float* out, float* part, int H,
+                                                               int D, int P, int window, int KS) {
+  using Lds = AttnLds<DT>;
+  constexpr int NKK = DT * 16;
   extern __shared__ float sm[];
-  float* qs = sm;              // [TQ][D]
-  float* S = sm + TQ * DMAX;   // [TQ][P]
+  float* Qs = sm;
+  float* VM = sm + Lds::Q;
+  float* Rl = VM + Lds::VM;
+  float* PbAll = Rl + Lds::R;
 
   const int h = blockIdx.y;
-  const int b = blockIdx.z;
-  const int t0 = blockIdx.x * TQ;
+  const int b = blockIdx.z / KS;
+  const int ks = blockIdx.z - b * KS;
+  const int t0 = blockIdx.x * 32;
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
   const long long CP = (long long)H * D * P;
   const float* qb = qkv + (long long)b * 3 * CP + (long long)h * D * P;
   const float* kb = qb + CP;
   const float* vb = qb + 2 * CP;
+  const int nb = 2 * window + 1;
+  const int t = t0 + l32;
   const float sq = sqrtf((float)D);
 
-  for (int e = tid; e < TQ * D; e += 256) {
-    const int tq = e / D, d = e - tq * D;
-    const int t = t0 + tq;
-    qs[tq * DMAX + d] = (t < P) ? qb[(long long)d * P + t] / sq : 0.f;
+  // stage qs[d][t] = q[d][t0 + t] / sqrt(D)
+  for (int e = tid; e < Lds::Q; e += 256) {
+    const int d = e >> 5, j = e & 31;
+    Qs[e] = (d < D && t0 + j < P) ? qb[(long long)d * P + t0 + j] / sq : 0.f;
+  }
+  float* Pb = PbAll + wave * 32 * 32;
+  for (int e = lane; e < 32 * 32; e += 64) Pb[e] = 0.f;
+  __syncthreads();
+  // R^T[r][t] = emb_k[r] . qs_t   (wave 0)
+  if (wave == 0) {
+    floatx16 racc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) racc[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const int d = 2 * kk + half;
+      const float a = (l32 < nb && d < D) ? emb_k[l32 * D + d] : 0.f;
+      racc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Qs[d * 32 + l32], racc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Rl[acc_row(r, half) * 32 + l32] = racc[r];
   }
   __syncthreads();
 
-  // scores
-  for (int s = tid; s < P; s += 256) {
-    float acc[TQ];
+  float* Vt = VM + wave * Lds::ROWS * Lds::VSTRIDE;
+  floatx16 O[DT];
 #pragma unroll
-    for (int tq = 0; tq < TQ; ++tq) acc[tq] = 0.f;
-    for (int d = 0; d < D; ++d) {
-      const float kv = kb[(long long)d * P + s];
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int tq = 0; tq < TQ; ++tq) acc[tq] += qs[tq * DMAX + d] * kv;
+    for (int r = 0; r < 16; ++r) O[dt][r] = 0.f;
+  float m = -INFINITY;  // running max of query t (same in both half-waves)
+  float l = 0.f;        // running sum over this half-wave's key rows
+
+  const int ntile = (P + 31) / 32;
+  const int per = (ntile + KS - 1) / KS;
+  const int kt_end = min(ntile, (ks + 1) * per);
+  for (int kt = ks * per + wave; kt < kt_end; kt += AWAVES) {
+    const int s0 = kt * 32;
+    // all global loads of the tile first: K operands and the V tile
+    const bool key_ok = s0 + l32 < P;
+    float kreg[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const int d = 2 * kk + half;
+      kreg[kk] = (d < D && key_ok) ? kb[(long long)d * P + s0 + l32] : 0.f;
     }
+    float vreg[DT * 16];
 #pragma unroll
-    for (int tq = 0; tq < TQ; ++tq) {
-      const int r = s - (t0 + tq);
-      if (r >= -window && r <= window) {
-        const float* e = emb_k + (long long)(r + window) * D;
-        float a2 = 0.f;
-        for (int d = 0; d < D; ++d) a2 += qs[tq * DMAX + d] * e[d];
-        acc[tq] = acc[tq] + a2;
+    for (int i = 0; i < DT * 16; ++i) {
+      const int e = lane + 64 * i;
+      const int d = e >> 5, j = e & 31;
+      vreg[i] = (d < D && s0 + j < P) ? vb[(long long)d * P + s0 + j] : 0.f;
+    }
+    // S^T[s][t] = sum_d k[d][s] qs[d][t]
+    floatx16 S;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kreg[kk], Qs[(2 * kk + half) * 32 + l32], S, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < DT * 16; ++i) {
+      const int e = lane + 64 * i;
+      Vt[(e >> 5) * Lds::VSTRIDE + (e & 31)] = vreg[i];
+    }
+    // band terms and key mask
+    const bool near = s0 <= t0 + 31 + window && s0 + 31 >= t0 - window;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int s = s0 + acc_row(r, half);
+      float v = S[r];
+      if (near) {
+        const int rr = s - t + window;
+        if (rr >= 0 && rr < nb) v = v + Rl[rr * 32 + l32];
       }
-      S[tq * P + s] = acc[tq];
+      S[r] = s < P ? v : -INFINITY;
     }
-  }
-  __syncthreads();
-
-  // softmax, two query rows per wave
-  const int wave = tid >> 6, lane = tid & 63;
-  for (int tq = wave; tq < TQ; tq += 4) {
-    float* row = S + tq * P;
-    float m = -INFINITY;
-    for (int s = lane; s < P; s += 64) m = fmaxf(m, row[s]);
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    // online softmax statistics of query t
+    float tm = S[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) tm = fmaxf(tm, S[r]);
+    tm = fmaxf(tm, __shfl_xor(tm, 32));
+    const float m_new = fmaxf(m, tm);
+    const float alpha = expf(m - m_new);
     float sum = 0.f;
-    for (int s = lane; s < P; s += 64) {
-      const float e = expf(row[s] - m);
-      row[s] = e;
-      sum += e;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = expf(S[r] - m_new);
+      S[r] = p;
+      sum += p;
     }
-    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
-    for (int s = lane; s < P; s += 64) row[s] = row[s] / sum;
+    l = l * alpha + sum;
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) O[dt][r] *= alpha;
+    if (half == 0 && alpha != 1.f)
+      for (int rr = 0; rr < nb; ++rr) Pb[rr * 32 + l32] *= alpha;
+    if (near) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = s0 + acc_row(r, half) - t + window;
+        if (rr >= 0 && rr < nb) Pb[rr * 32 + l32] += S[r];
+      }
+    }
+    // O^T[d][t] += sum_s V[d][s] P^T[s][t]
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const float* vrow = Vt + (dt * 32 + l32) * Lds::VSTRIDE;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        O[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[acc_row(r, half)], S[r], O[dt], 0, 0, 0);
+    }
+  }
+
+  // band contribution: O^T[d][t] += sum_r emb_v[r][d] Pb[r][t]
+  for (int kk = 0; kk < (nb + 1) / 2; ++kk) {
+    const int rr = 2 * kk + half;
+    const float bval = rr < nb ? Pb[rr * 32 + l32] : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d = dt * 32 + l32;
+      const float a = (rr < nb && d < D) ? emb_v[rr * D + d] : 0.f;
+      O[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bval, O[dt], 0, 0, 0);
+    }
+  }
+  l = l + __shfl_xor(l, 32);
+
+  // merge the four waves: M = max m_w, L = sum l_w e^(m_w-M), O = sum O_w e^(m_w-M)
+  __syncthreads();  // V tiles are dead; reuse their LDS for the merge
+  constexpr int PER = DT * 16 * 64 + 2 * 32;
+  if (wave > 0) {
+    float* dst = VM + (wave - 1) * PER;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[(dt * 16 + r) * 64 + lane] = O[dt][r];
+    if (half == 0) {
+      dst[DT * 16 * 64 + l32] = m;
+      dst[DT * 16 * 64 + 32 + l32] = l;
+    }
   }
   __syncthreads();
-
-  // weighted sums
-  for (int e = tid; e < TQ * D; e += 256) {
-    const int tq = e / D, d = e - tq * D;
-    const int t = t0 + tq;
-    if (t >= P) continue;
-    const float* row = S + tq * P;
-    const float* vr = vb + (long long)d * P;
-    float acc = 0.f;
-    for (int s = 0; s < P; ++s) acc += row[s] * vr[s];
-    float a2 = 0.f;
-    const int s_lo = max(0, t - window), s_hi = min(P - 1, t + window);
-    for (int s = s_lo; s <= s_hi; ++s) a2 += row[s] * emb_v[(long long)(s - t + window) * D + d];
-    out[(long long)b * H * D * P + (long long)(h * D + d) * P + t] = acc + a2;
+  if (wave > 0) return;
+  float M = m;
+  for (int w = 1; w < AWAVES; ++w) M = fmaxf(M, VM[(w - 1) * PER + DT * 16 * 64 + l32]);
+  // a slice with no keys at all keeps M = -inf; its partial carries zero weight
+  const float f0 = M == -INFINITY ? 0.f : expf(m - M);
+  float L = l * f0;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) O[dt][r] *= f0;
+  for (int w = 1; w < AWAVES; ++w) {
+    const float* src = VM + (w - 1) * PER;
+    const float mw = src[DT * 16 * 64 + l32];
+    const float f = M == -INFINITY ? 0.f : expf(mw - M);
+    L += src[DT * 16 * 64 + 32 + l32] * f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) O[dt][r] += src[(dt * 16 + r) * 64 + lane] * f;
   }
+  if (t >= P) return;
+  if (KS == 1) {
+    float* ob = out + (long long)b * H * D * P + (long long)h * D * P;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dt * 32 + acc_row(r, half);
+        if (d < D) ob[(long long)d * P + t] = O[dt][r] / L;
+      }
+  } else {
+    // partial slice: part[((b*H + h)*KS + ks)] holds m[P], l[P], O[D][P]
+    float* pb = part + ((long long)(b * H + h) * KS + ks) * (long long)(D + 2) * P;
+    if (half == 0) {
+      pb[t] = M;
+      pb[P + t] = L;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = dt * 32 + acc_row(r, half);
+        if (d < D) pb[(long long)(2 + d) * P + t] = O[dt][r];
+      }
+  }
+}
+
+// out[b][h*D+d][t] = sum_ks O_ks e^(m_ks - M) / sum_ks l_ks e^(m_ks - M)
+__global__ __launch_bounds__(256) void relpos_attention_merge(const float* part, float* out, int H, int D, int P,
+                                                              int KS, long long n) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int t = (int)(e % P);
+  const long long r = e / P;
+  const int d = (int)(r % D);
+  const long long bh = r / D;
+  const float* pb = part + bh * KS * (long long)(D + 2) * P;
+  float M = -INFINITY;
+  for (int k = 0; k < KS; ++k) M = fmaxf(M, pb[k * (long long)(D + 2) * P + t]);
+  float L = 0.f, O = 0.f;
+  for (int k = 0; k < KS; ++k) {
+    const float* s = pb + k * (long long)(D + 2) * P;
+    const float f = s[t] == -INFINITY ? 0.f : expf(s[t] - M);
+    L += s[P + t] * f;
+    O += s[(long long)(2 + d) * P + t] * f;
+  }
+  out[(bh * D + d) * (long long)P + t] = O / L;
+}
+
+template <int DT>
+void launch_dt(const float* qkv, const float* emb_k, const float* emb_v, float* out, float* part, int B, int H,
+               int D, int P, int window, int KS, hipStream_t s) {
+  const size_t lds = sizeof(float) * AttnLds<DT>::TOTAL;
+  static bool attr = false;
+  if (!attr) {
+    RVC_HIP(hipFuncSetAttribute((const void*)relpos_attention_kernel<DT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    attr = true;
+  }
+  dim3 grid((P + 31) / 32, H, B * KS);
+  hipLaunchKernelGGL(relpos_attention_kernel<DT>, grid, dim3(256), lds, s, qkv, emb_k, emb_v, out, part, H, D, P,
+                     window, KS);
+  check_launch("relpos_attention");
 }
 
 }  // namespace
 
-size_t relpos_attention_max_frames() { return (kLdsMax / sizeof(float) - TQ * DMAX) / TQ; }
+int relpos_attention_splits(int B, int H, int P) {
+  const int ntile = (P + 31) / 32;
+  const int blocks = ((P + 31) / 32) * H * B;
+  int ks = (256 + blocks - 1) / blocks;
+  ks = std::min(ks, std::max(1, ntile / AWAVES));
+  return std::max(ks, 1);
+}
 
-void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out, int B,
-                             int H, int D, int P, int window, hipStream_t s) {
-  RVC_CHECK(D >= 1 && D <= DMAX, "relpos_attention: head dim must be in [1,128]");
-  RVC_CHECK(P >= 1 && (size_t)P <= relpos_attention_max_frames(),
-            "relpos_attention: too many frames for the LDS score rows");
-  const size_t lds = sizeof(float) * ((size_t)TQ * DMAX + (size_t)TQ * P);
-  dim3 grid((P + TQ - 1) / TQ, H, B);
-  hipLaunchKernelGGL(relpos_attention_kernel, grid, dim3(256), lds, s, qkv, emb_k, emb_v, out, H, D, P,
-                     window);
-  check_launch("relpos_attention");
+size_t relpos_attention_scratch_floats(int B, int H, int D, int P) {
+  const int ks = relpos_attention_splits(B, H, P);
+  return ks > 1 ? (size_t)B * H * ks * (D + 2) * P : 0;
+}
+
+size_t relpos_attention_max_frames() { return (size_t)1 << 30; }
+
+void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out, float* scratch,
+                             int B, int H, int D, int P, int window, hipStream_t s) {
+  RVC_CHECK(D >= 1 && D <= 128, "relpos_attention: head dim must be in [1,128]");
+  RVC_CHECK(window >= 0 && window <= kMaxWindow, "relpos_attention: window must be in [0,15]");
+  RVC_CHECK(P >= 1 && B >= 1 && H >= 1, "relpos_attention: invalid shape");
+  const int KS = relpos_attention_splits(B, H, P);
+  RVC_CHECK(KS == 1 || scratch != nullptr, "relpos_attention: scratch buffer required");
+  const int dt = (D + 31) / 32;
+  if (dt == 1) launch_dt<1>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
+  else if (dt == 2) launch_dt<2>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
+  else if (dt == 3) launch_dt<3>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
+  else launch_dt<4>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
+  if (KS > 1) {
+    const long long n = (long long)B * H * D * P;
+    hipLaunchKernelGGL(relpos_attention_merge, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, scratch, out, H, D,
+                       P, KS, n);
+    check_launch("relpos_attention_merge");
+  }
 }
 
 }  // namespace rvc

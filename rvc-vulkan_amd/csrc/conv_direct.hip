@@ -22,49 +22,42 @@ __device__ __forceinline__ float act_out(float v, int act, float slope) {
   return v;
 }
 
-constexpr int kTI = 64;            // outputs per workgroup along time
-constexpr int kTCO = 4;            // output channels per workgroup
-constexpr int kWinFloats = 8192;   // LDS window budget (32 KB)
-
-// Workgroup (64 x 4 threads) computes kTI consecutive outputs for kTCO output
-// channels.  The input window of a chunk of channels is staged in LDS so the
-// strided taps read LDS instead of re-fetching global memory.
-__global__ __launch_bounds__(256) void conv1d_direct_kernel(DirectConvArgs a, int win, int cic) {
-  __shared__ float xs[kWinFloats];
-  const int tx = threadIdx.x & 63;
-  const int ty = threadIdx.x >> 6;
+// One thread per output position i, TCO output channels per workgroup: the
+// weights are uniform across the workgroup (scalar loads) and each input
+// sample is loaded once for all TCO channels.  Neighbouring threads' taps
+// overlap, so the input reads are served by the L1/L2 caches.
+template <int TCO>
+__global__ __launch_bounds__(256) void conv1d_direct_kernel(DirectConvArgs a) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int co0 = blockIdx.y * TCO;
   const int b = blockIdx.z;
-  const int i0 = blockIdx.x * kTI;
-  const int co = blockIdx.y * kTCO + ty;
-  const int i = i0 + tx;
+  if (i >= a.n_out) return;  // no barriers below
   const float* xb = a.x + (long long)b * a.xb;
-  const long long tbase = (long long)i0 * a.stride + a.in_off;
-  float acc = 0.f;
-  for (int ci0 = 0; ci0 < a.C_in; ci0 += cic) {
-    const int nci = min(cic, a.C_in - ci0);
-    __syncthreads();
-    for (int e = threadIdx.x; e < nci * win; e += 256) {
-      const int r = e / win;
-      const int j = e - r * win;
-      const long long t = tbase + j;
-      float v = 0.f;
-      if (t >= 0 && t < a.L_in) v = act_in(xb[(long long)(ci0 + r) * a.xc + t], a.in_act, a.in_slope);
-      xs[e] = v;
-    }
-    __syncthreads();
-    if (co < a.C_out && i < a.n_out) {
-      for (int r = 0; r < nci; ++r) {
-        const float* wr = a.w + ((long long)co * a.C_in + ci0 + r) * a.K;
-        const float* xr = xs + r * win + tx * a.stride;
-        for (int k = 0; k < a.K; ++k) acc += wr[k] * xr[k * a.dil];
+  float acc[TCO];
+#pragma unroll
+  for (int c = 0; c < TCO; ++c) acc[c] = 0.f;
+  const long long t0 = (long long)i * a.stride + a.in_off;
+  for (int ci = 0; ci < a.C_in; ++ci) {
+    const float* xr = xb + (long long)ci * a.xc;
+    for (int k = 0; k < a.K; ++k) {
+      const long long t = t0 + (long long)k * a.dil;
+      const float v = (t >= 0 && t < a.L_in) ? act_in(xr[t], a.in_act, a.in_slope) : 0.f;
+#pragma unroll
+      for (int c = 0; c < TCO; ++c) {
+        const int co = min(co0 + c, a.C_out - 1);
+        acc[c] += a.w[((long long)co * a.C_in + ci) * a.K + k] * v;
       }
     }
   }
-  if (co < a.C_out && i < a.n_out) {
-    float v = acc;
+  float* ob = a.out + (long long)b * a.ob + i;
+#pragma unroll
+  for (int c = 0; c < TCO; ++c) {
+    const int co = co0 + c;
+    if (co >= a.C_out) break;
+    float v = acc[c];
     if (a.bias) v = v + a.bias[co];
     v = act_out(v, a.out_act, a.out_slope);
-    float* o = a.out + (long long)b * a.ob + (long long)co * a.oc + i;
+    float* o = ob + (long long)co * a.oc;
     if (a.combine == COMB_ADD) v = *o + v;
     else if (a.combine == COMB_ADD_DIV) v = (*o + v) / a.div;
     *o = v;
@@ -128,11 +121,13 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
   RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.K >= 1 && a.stride >= 1 && a.dil >= 1 && a.B >= 1,
             "conv1d_direct: invalid shape");
   if (a.n_out <= 0) return;
-  const int win = (kTI - 1) * a.stride + (a.K - 1) * a.dil + 1;
-  RVC_CHECK(win <= kWinFloats, "conv1d_direct: input window too large for LDS");
-  const int cic = kWinFloats / win;
-  dim3 grid((a.n_out + kTI - 1) / kTI, (a.C_out + kTCO - 1) / kTCO, a.B);
-  hipLaunchKernelGGL(conv1d_direct_kernel, grid, dim3(256), 0, s, a, win, cic);
+  if (a.C_out >= 8) {
+    dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);
+    hipLaunchKernelGGL(conv1d_direct_kernel<8>, grid, dim3(256), 0, s, a);
+  } else {
+    dim3 grid((a.n_out + 255) / 256, a.C_out, a.B);
+    hipLaunchKernelGGL(conv1d_direct_kernel<1>, grid, dim3(256), 0, s, a);
+  }
   check_launch("conv1d_direct");
 }
 

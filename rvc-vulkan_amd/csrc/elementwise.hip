@@ -201,24 +201,29 @@ __global__ void gather_rows_i64_kernel(const long long* ids, const float* table,
   }
 }
 
-__global__ void gemv_kernel(const float* W, const float* bias, const float* g, long long gb, float* out,
-                            long long ob, int C_out, int C_in, long long n) {
-  GRID_STRIDE(e, n) {
-    const int co = (int)(e % C_out);
-    const long long b = e / C_out;
-    const float* gg = g + b * gb;
-    const float* wr = W + (long long)co * C_in;
-    float acc = 0.f;
-    for (int ci = 0; ci < C_in; ++ci) acc += wr[ci] * gg[ci];
-    out[b * ob + co] = acc + bias[co];
-  }
+// One wave per output row: lanes stride the row (coalesced), then a
+// butterfly reduction.
+__global__ __launch_bounds__(256) void gemv_kernel(const float* W, const float* bias, const float* g, long long gb,
+                                                   float* out, long long ob, int C_out, int C_in, long long n) {
+  const long long e = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (e >= n) return;
+  const int co = (int)(e % C_out);
+  const long long b = e / C_out;
+  const float* gg = g + b * gb;
+  const float* wr = W + (long long)co * C_in;
+  float acc = 0.f;
+  for (int ci = lane; ci < C_in; ci += 64) acc += wr[ci] * gg[ci];
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) out[b * ob + co] = acc + bias[co];
 }
 
 // ---- NSF sine source (runtime/models/vits.py:1468-1501) ----
 // Phase offsets: acc[p] = fmod(cumsum_{q<=p} rad2[q], 1) where
 // rad2[q] = fmod(f0[q]/sr*upp + 0.5, 1) - 0.5.  The cumulative sum is a
-// sequential float32 recurrence (numpy's cumsum order), so one thread per
-// batch item walks the frames after the block has staged f0 in LDS.
+// sequential float32 recurrence (numpy's cumsum order): after the workgroup
+// has staged rad2 in LDS, one thread runs the additions alone and the fmod
+// of every prefix is taken in parallel afterwards.
 __global__ __launch_bounds__(256) void sine_phase_kernel(const float* f0, float* acc, int P, int upp,
                                                          float sr) {
   extern __shared__ float r2[];
@@ -230,13 +235,15 @@ __global__ __launch_bounds__(256) void sine_phase_kernel(const float* f0, float*
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float c = 0.f;
-    float* ab = acc + (long long)b * P;
-    for (int p = 0; p < P; ++p) {
-      c = (p == 0) ? r2[0] : c + r2[p];
-      ab[p] = fmodf(c, 1.0f);
+    float c = r2[0];
+    for (int p = 1; p < P; ++p) {
+      c = c + r2[p];
+      r2[p] = c;
     }
   }
+  __syncthreads();
+  float* ab = acc + (long long)b * P;
+  for (int p = threadIdx.x; p < P; p += blockDim.x) ab[p] = fmodf(r2[p], 1.0f);
 }
 
 // har[b][p*upp+u] = tanh(w * (0.1*sin(2pi*rad)*uv + amp*ns) + b) with
@@ -381,7 +388,7 @@ void launch_gemv(const float* W, const float* bias, const float* g, long long gb
                  int B, int C_out, int C_in, hipStream_t s) {
   const long long n = (long long)B * C_out;
   if (n <= 0) return;
-  hipLaunchKernelGGL(gemv_kernel, dim3(capped_grid(n)), dim3(256), 0, s, W, bias, g, gb, out, ob, C_out,
+  hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, W, bias, g, gb, out, ob, C_out,
                      C_in, n);
   check_launch("gemv");
 }

@@ -200,9 +200,12 @@ void launch_softmax_rows(const float* x, float* out, long long rows, int cols, h
 
 // ---------------------------------------------------------------- attention
 // Windowed relative-position attention, all heads.
-// qkv[b][3*H*D][P] (q, k, v stacked), emb_k/emb_v [2w+1][D], out[b][H*D][P].
+// qkv[b][3*H*D][P] (q, k, v stacked), emb_k/emb_v [2w+1][D], out[b][H*D][P];
+// scratch holds relpos_attention_scratch_floats(B,H,D,P) floats (may be
+// null when that is 0).
 void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out,
-                             int B, int H, int D, int P, int window, hipStream_t s);
+                             float* scratch, int B, int H, int D, int P, int window, hipStream_t s);
+size_t relpos_attention_scratch_floats(int B, int H, int D, int P);
 size_t relpos_attention_max_frames();
 
 // ---------------------------------------------------------------- matmul

@@ -56,29 +56,54 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const float* x, con
   for (int c = threadIdx.x; c < cols; c += blockDim.x) orow[c] = (xr[c] - mean) / den * g[c] + b[c];
 }
 
-// Channel-major [B][C][L]: normalise over C for each (b, t); one thread per
-// column, consecutive threads on consecutive t so every channel read is
-// coalesced.
-__global__ __launch_bounds__(256) void layernorm_cols_kernel(const float* x, const float* g, const float* b,
-                                                             float* out, int C, int L, float eps,
-                                                             long long n) {
-  const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  const long long bi = e / L;
-  const int t = (int)(e - bi * L);
-  const float* xc = x + bi * (long long)C * L + t;
-  float* oc = out + bi * (long long)C * L + t;
+// Channel-major [B][C][L]: normalise over C for each (b, t).  A workgroup
+// owns LN_COLS consecutive columns; its LN_GRP thread groups split the
+// channels (coalesced reads along t) and combine partial sums in LDS.
+constexpr int LN_COLS = 32;
+constexpr int LN_GRP = 8;
+
+__global__ __launch_bounds__(LN_COLS * LN_GRP) void layernorm_cols_kernel(const float* x, const float* g,
+                                                                          const float* b, float* out, int C,
+                                                                          int L, float eps) {
+  __shared__ double part[LN_GRP][LN_COLS];
+  __shared__ float stat[2][LN_COLS];
+  const int tx = threadIdx.x % LN_COLS;
+  const int ty = threadIdx.x / LN_COLS;
+  const int t = blockIdx.x * LN_COLS + tx;
+  const long long base = (long long)blockIdx.y * C * L;
+  const bool ok = t < L;
+  const float* xc = x + base + t;
   double s = 0.0;
-  for (int c = 0; c < C; ++c) s += xc[(long long)c * L];
-  const float mean = (float)(s / C);
-  double v = 0.0;
-  for (int c = 0; c < C; ++c) {
-    const float d = xc[(long long)c * L] - mean;
-    v += (double)d * d;
+  if (ok)
+    for (int c = ty; c < C; c += LN_GRP) s += xc[(long long)c * L];
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0) {
+    double tot = 0.0;
+    for (int i = 0; i < LN_GRP; ++i) tot += part[i][tx];
+    stat[0][tx] = (float)(tot / C);
   }
-  const float var = (float)(v / C);
-  const float den = sqrtf(var + eps);
-  for (int c = 0; c < C; ++c) oc[(long long)c * L] = (xc[(long long)c * L] - mean) / den * g[c] + b[c];
+  __syncthreads();
+  const float mean = stat[0][tx];
+  double v = 0.0;
+  if (ok)
+    for (int c = ty; c < C; c += LN_GRP) {
+      const float d = xc[(long long)c * L] - mean;
+      v += (double)d * d;
+    }
+  part[ty][tx] = v;
+  __syncthreads();
+  if (ty == 0) {
+    double tot = 0.0;
+    for (int i = 0; i < LN_GRP; ++i) tot += part[i][tx];
+    stat[1][tx] = sqrtf((float)(tot / C) + eps);
+  }
+  __syncthreads();
+  const float den = stat[1][tx];
+  if (ok) {
+    float* oc = out + base + t;
+    for (int c = ty; c < C; c += LN_GRP) oc[(long long)c * L] = (xc[(long long)c * L] - mean) / den * g[c] + b[c];
+  }
 }
 
 __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* x, float* out, int cols) {
@@ -112,10 +137,9 @@ void launch_layernorm_rows(const float* x, const float* g, const float* b, float
 
 void launch_layernorm_cols(const float* x, const float* g, const float* b, float* out, int B, int C, int L,
                            float eps, hipStream_t s) {
-  const long long n = (long long)B * L;
-  if (n <= 0 || C <= 0) return;
-  hipLaunchKernelGGL(layernorm_cols_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, g, b, out,
-                     C, L, eps, n);
+  if ((long long)B * L <= 0 || C <= 0) return;
+  dim3 grid((L + LN_COLS - 1) / LN_COLS, B);
+  hipLaunchKernelGGL(layernorm_cols_kernel, grid, dim3(LN_COLS * LN_GRP), 0, s, x, g, b, out, C, L, eps);
   check_launch("layernorm_cols");
 }
 
