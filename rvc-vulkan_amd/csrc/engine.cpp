@@ -48,7 +48,9 @@ Engine::Engine() {
   RVC_HIP(hipGetDevice(&device));
   hipDeviceProp_t prop;
   RVC_HIP(hipGetDeviceProperties(&prop, device));
-  device_name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+  // some drivers leave the marketing name empty; the ISA name is always set
+  const std::string nm = prop.name[0] ? std::string(prop.name) : std::string("AMD GPU");
+  device_name = nm + " (" + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) + " CUs)";
   RVC_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
 }
 

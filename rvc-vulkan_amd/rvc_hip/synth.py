@@ -46,8 +46,19 @@ def _i64(a):
 class HipSynthesizer:
     """RVC v2 synthesizer with every weight resident on one MI355X."""
 
-    def __init__(self, w: dict, config=None, sr: int | None = None, ctx: HipContext | None = None):
+    def __init__(self, w: dict, config=None, sr: int | None = None, ctx: HipContext | None = None,
+                 geometry=None):
+        """``config`` / ``sr`` derive the geometry like the reference's
+        ``VitsConfig``; ``geometry`` (any object with ``upsample_rates``,
+        ``upsample_kernels`` and ``sr``, e.g. a reference ``VitsConfig``)
+        overrides those three."""
         self.cfg = VitsConfig(w, config, sr=sr)
+        if geometry is not None:
+            self.cfg.upsample_rates = [int(r) for r in geometry.upsample_rates]
+            self.cfg.upsample_kernels = [int(k) for k in geometry.upsample_kernels]
+            self.cfg.sr = int(geometry.sr)
+            self.cfg.n_ups = len(self.cfg.upsample_rates)
+            self.cfg.upp = int(np.prod(self.cfg.upsample_rates))
         self.ctx = ctx or get_context()
         self._lib = _hip.get_lib()
         self.handle = int(self._lib.rvc_synth_create(self.ctx.handle))
