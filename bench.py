@@ -66,13 +66,40 @@ def cpu_baseline(w, geom):
                       f"numpy oracle, 1 run after a warm-up, {dt:.2f} s wall"}
 
 
+def calibrate_copy(mib: int):
+    """rvc_copy of ``mib`` MiB, 5 launches: each reads and writes exactly
+    ``mib`` MiB, so FETCH_SIZE / WRITE_SIZE per dispatch should read
+    ``mib * 1024`` KiB; the ratio scales the counters of the other kernels."""
+    from rvc_hip import _hip
+    from rvc_hip.hip_ops import get_context
+
+    ctx = get_context()
+    n = mib * (1 << 20) // 4
+    src = ctx.upload(np.random.default_rng(0).standard_normal(n).astype(np.float32))
+    dst = ctx.alloc(n)
+    lib = _hip.get_lib()
+    for _ in range(5):
+        _hip._check(lib.rvc_copy(ctx.handle, dst, src, n), "rvc_copy")
+    ctx.download(dst, (4,))
+    print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 5}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quick", action="store_true",
+                    help="only the timed steps (no per-family breakdown, host-I/O rate or CPU baseline); "
+                         "for profiler runs")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run the library's plain copy kernel (rvc_copy) 5 times on "
+                         "a MIB-sized buffer: the reference reading for the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -136,7 +163,7 @@ def main():
 
     # per-family breakdown (one extra untimed step per family)
     breakdown = {}
-    for tag in ("dec.rb.s0", "dec.rb.s1", "dec.rb.s2", "dec.rb.s3", "dec.avg", "dec.ups", "dec.noise", "dec.post",
+    for tag in () if args.quick else ("dec.rb.s0", "dec.rb.s1", "dec.rb.s2", "dec.rb.s3", "dec.avg", "dec.ups", "dec.noise", "dec.post",
                 "dec.sine", "dec.pre", "enc", "flow"):
         s.set_timing(tag)
         step()
@@ -147,12 +174,14 @@ def main():
     s.set_timing("")
 
     # PCIe-inclusive rate (host numpy in -> host numpy out); reported, never the headline
-    t0 = time.perf_counter()
-    for _ in range(3):
-        s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
-    host_io = audio_s * 3 / (time.perf_counter() - t0)
+    host_io = None
+    if not args.quick:
+        t0 = time.perf_counter()
+        for _ in range(3):
+            s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
+        host_io = round(audio_s * 3 / (time.perf_counter() - t0), 2)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(w, geom)
+    cpu = None if (args.no_cpu_baseline or args.quick) else cpu_baseline(w, geom)
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -160,7 +189,7 @@ def main():
         "config": {"workload": "config 2: RVC v2 40k enc_p+flow+GeneratorNSF, 10 s (P=1000), batch 1, fp32",
                    "frames": P, "batch": B, "sample_rate": SR, "output_samples": n_out},
         "roofline": roofline, "cpu_baseline": cpu,
-        "host_io_audio_s_per_s": round(host_io, 2), "breakdown": breakdown,
+        "host_io_audio_s_per_s": host_io, "breakdown": breakdown,
     }
     print(json.dumps(line), flush=True)
 

@@ -29,6 +29,13 @@ than itself; the tests named here live under ``tests/``):
 * ``GeneratorNSF.sine_gen``: special cases (f0 == 0, constant f0) and the
   golden vectors written by importing the reference
   (``tests/golden/make_golden.py``).
+* ``hubert_ref.gelu_erf``: the reference's own outputs on a grid and the
+  exact-erf GELU within the A&S 7.1.26 bound; ``group_norm``: a float64
+  per-group standardisation; ``pos_conv_weight``: the ``g = ||v||`` case;
+  ``grouped_conv1d``: the equivalent block-diagonal dense conv;
+  ``HubertRef`` stages (conv stack, projection, encoder entry, layer 1,
+  version 1 and 2 outputs): reference golden vectors at T in {1600, 4000}
+  (``tests/golden/make_golden_hubert.py``; test_oracle_hubert.py).
 * ``VitsConfig``, ``TextEncoder.encode``, ``FlowBlock.reverse``,
   ``GeneratorNSF.forward`` and ``Synthesizer.infer_controlled``: golden
   vectors produced by the reference's own numpy code at reduced and full

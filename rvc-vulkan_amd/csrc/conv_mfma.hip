@@ -291,9 +291,13 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   if (max_n_out(a) == 0) return;
   // Tile choice: widest co tile that divides C_out while the grid still
   // gives every CU work (256 CUs); few output columns -> split-K waves.
+  // The 128 x 128 tile (two resident workgroups per CU) also needs about two
+  // rounds of workgroups, or the longest-tap groups of a grouped launch set
+  // the makespan (measured: the C = 256 decoder stage runs 10 % faster on
+  // 64 x 128 tiles).
   const long long want = 384;
   bool ok = false;
-  if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= want) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
+  if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)
     ok = launch_cfg<64, 128, 32, 64, 16, 1>(a, s) || launch_cfg<64, 128, 32, 64, 8, 1>(a, s);
   if (!ok && a.C_out <= 32 && n_blocks(a, 32, 256) >= want)

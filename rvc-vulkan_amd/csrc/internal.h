@@ -69,6 +69,7 @@ struct ConvGroup {
   int out_off;
   int n_out;
   int combine;
+  int tiles;          // output tiles per workgroup (set by the launcher)
 };
 
 // A launch of up to kMaxConvGroups convolutions with the same channel

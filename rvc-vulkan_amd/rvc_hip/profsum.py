@@ -45,7 +45,7 @@ def kernel_rows(db: str):
 
 def pmc_rows(db: str):
     con = sqlite3.connect(db)
-    q = ("select k.name, k.grid_x, k.grid_y, k.grid_z, k.workgroup_x, p.counter_name, avg(p.value), count(*) "
+    q = ("select k.name, k.grid_x, k.grid_y, k.grid_z, k.workgroup_x, p.counter_name, avg(p.counter_value), count(*) "
          "from pmc_events p join kernels k on p.event_id = k.id "
          "group by k.name, k.grid_x, k.grid_y, k.grid_z, p.counter_name")
     out = []

@@ -39,6 +39,10 @@ __all__ = [
     "make_synth_inputs",
     "make_noise",
     "weights_digest",
+    "HubertGeometry",
+    "HUBERT_BASE",
+    "make_hubert_weights",
+    "make_hubert_input",
 ]
 
 
@@ -273,3 +277,90 @@ def make_synth_inputs(geom: Geometry, P: int, seed: int):
     nz, ns = make_noise(geom, P, seed)
     return {"phone": phone, "pitch": pitch, "nsff0": nsff0, "sid": sid,
             "nz": nz, "ns": ns}
+
+
+# ---------------------------------------------------------------------------
+# HuBERT-base
+# ---------------------------------------------------------------------------
+
+class HubertGeometry:
+    """HuBERT-base hyper-parameters as the reference fixes them
+    (``runtime/models/hubert.py:9-44``): 7 conv layers of 512 channels,
+    kernels [10,3,3,3,3,2,2] / strides [5,2,2,2,2,2,2], GroupNorm on layer 0,
+    hidden 768, 12 layers, 12 heads, FFN 3072, pos-conv k128 in 16 groups."""
+
+    def __init__(self, *, conv_dim=512, conv_kernels=(10, 3, 3, 3, 3, 2, 2), hidden=768, n_layers=12,
+                 ffn=3072, pos_kernel=128, pos_groups=16, final_dim=256):
+        self.conv_dim = conv_dim
+        self.conv_kernels = list(conv_kernels)
+        self.conv_strides = [5] + [2] * (len(conv_kernels) - 1)
+        self.hidden = hidden
+        self.n_layers = n_layers
+        self.ffn = ffn
+        self.pos_kernel = pos_kernel
+        self.pos_groups = pos_groups
+        self.final_dim = final_dim
+
+    def frames(self, T: int) -> int:
+        L = T
+        for k, s in zip(self.conv_kernels, self.conv_strides):
+            L = (L - k) // s + 1
+        return L
+
+
+HUBERT_BASE = HubertGeometry()
+
+
+def make_hubert_weights(geom: HubertGeometry = HUBERT_BASE, seed: int = 0) -> dict:
+    """Random-init float32 state dict with the transformers key names the
+    reference reads (``runtime/models/hubert.py:510-558``).
+
+    Convs: ``N(0, sqrt(2 / fan_in))`` (keeps the bias-free conv + GELU stack
+    away from underflow); linears: ``U(+-1/sqrt(fan_in))`` weights and biases;
+    norms: ``gamma ~ 1 + 0.1 N``, ``beta ~ 0.1 N``; the positional conv's
+    ``weight_g`` is the per-tap norm of ``weight_v`` times ``U(0.8, 1.2)``."""
+    rng = np.random.default_rng(seed)
+    w: dict = {}
+    C, H, F = geom.conv_dim, geom.hidden, geom.ffn
+
+    def norm_pair(name, n):
+        w[name + ".weight"] = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        w[name + ".bias"] = (0.1 * rng.standard_normal(n)).astype(np.float32)
+
+    def linear(name, o, i):
+        w[name + ".weight"] = _uniform(rng, (o, i), i)
+        w[name + ".bias"] = _uniform(rng, (o,), i)
+
+    c_in = 1
+    for i, k in enumerate(geom.conv_kernels):
+        w[f"feature_extractor.conv_layers.{i}.conv.weight"] = (
+            rng.standard_normal((C, c_in, k)) * math.sqrt(2.0 / (c_in * k))).astype(np.float32)
+        c_in = C
+    norm_pair("feature_extractor.conv_layers.0.layer_norm", C)
+    norm_pair("feature_projection.layer_norm", C)
+    linear("feature_projection.projection", H, C)
+    cpg = H // geom.pos_groups
+    K = geom.pos_kernel
+    v = (rng.standard_normal((H, cpg, K)) / math.sqrt(cpg * K)).astype(np.float32)
+    tap_norm = np.sqrt((v.astype(np.float64) ** 2).sum(axis=(0, 1)))
+    w["encoder.pos_conv_embed.conv.weight_v"] = v
+    w["encoder.pos_conv_embed.conv.weight_g"] = (tap_norm * rng.uniform(0.8, 1.2, size=K)).astype(
+        np.float32).reshape(1, 1, K)
+    w["encoder.pos_conv_embed.conv.bias"] = _uniform(rng, (H,), cpg * K)
+    norm_pair("encoder.layer_norm", H)
+    for i in range(geom.n_layers):
+        p = f"encoder.layers.{i}."
+        for nm in ("q_proj", "k_proj", "v_proj", "out_proj"):
+            linear(p + "attention." + nm, H, H)
+        norm_pair(p + "layer_norm", H)
+        linear(p + "feed_forward.intermediate_dense", F, H)
+        linear(p + "feed_forward.output_dense", H, F)
+        norm_pair(p + "final_layer_norm", H)
+    linear("final_proj", geom.final_dim, H)
+    return w
+
+
+def make_hubert_input(T: int, seed: int) -> np.ndarray:
+    """BASELINE config 3 input: x ~ N(0, 0.1) [1, T] at 16 kHz."""
+    rng = np.random.default_rng(seed)
+    return (0.1 * rng.standard_normal((1, T))).astype(np.float32)
