@@ -158,6 +158,29 @@ int32_t rvc_synth_set_debug(int64_t s, int32_t keep_stages);
 int32_t rvc_synth_set_timing(int64_t s, const char* tag);
 int32_t rvc_synth_get_timing(int64_t s, double* total_ms, int64_t* launches, double* flops, double* bytes);
 
+/* ---------------------------------------------------------------- HuBERT session
+ * No counterpart in the reference ABI.  A device-resident HuBERT-base encoder:
+ * HubertEncoder.encode (runtime/models/hubert.py:564-591) as one stream of HIP
+ * kernels over weights uploaded once.  Weights are registered under their
+ * transformers state-dict keys (runtime/models/hubert.py:524-558); the
+ * positional conv's weight norm is resolved at finalize (:510-522). */
+int64_t rvc_hubert_create(int64_t h);
+int32_t rvc_hubert_destroy(int64_t s);
+int32_t rvc_hubert_set_weight(int64_t s, const char* key, const float* data, const int64_t* shape, int32_t ndim);
+int32_t rvc_hubert_finalize(int64_t s);
+/* Output frames L of the feature extractor for T input samples. */
+int32_t rvc_hubert_frames(int64_t s, int64_t T, int64_t* L);
+/* x [B,T] float32 16 kHz -> out [B,L,768] (version 2, last hidden state) or
+ * [B,L,256] (version 1, final_proj of layer 9). */
+int32_t rvc_hubert_encode(int64_t s, const float* x, int64_t B, int64_t T, int32_t version, float* out);
+int32_t rvc_hubert_encode_dev(int64_t s, int64_t x, int64_t B, int64_t T, int32_t version, int64_t out);
+/* Named intermediates of the last call, channel-major [B,C,L]: "feats",
+ * "proj", "pos", "entry", and "layer1" after rvc_hubert_set_debug(s, 1). */
+int32_t rvc_hubert_read(int64_t s, const char* name, float* dst, int64_t n);
+int32_t rvc_hubert_set_debug(int64_t s, int32_t keep);
+int32_t rvc_hubert_set_timing(int64_t s, const char* tag);
+int32_t rvc_hubert_get_timing(int64_t s, double* total_ms, int64_t* launches, double* flops, double* bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,7 +10,9 @@
 //
 // emb_rel is zero outside the window after _get_relative_embeddings
 // (runtime/models/vits.py:448-462), so only the 2w+1 band diagonals carry the
-// relative terms.
+// relative terms.  With emb_k == emb_v == null the band terms vanish and the
+// kernel is plain scaled-dot-product attention (HuBERT's self-attention,
+// q scaled by 1/sqrt(D), runtime/models/hubert.py:1315-1338).
 //
 // A workgroup owns 32 queries of one head and one slice of the keys (the key
 // axis is split over KS workgroups so short sequences still fill the GPU);
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   const float* qb = qkv + (long long)b * 3 * CP + (long long)h * D * P;
   const float* kb = qb + CP;
   const float* vb = qb + 2 * CP;
-  const int nb = 2 * window + 1;
+  const int nb = emb_k != nullptr ? 2 * window + 1 : 0;  // no band: plain attention
   const int t = t0 + l32;
   const float sq = sqrtf((float)D);
 
@@ -336,6 +338,7 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
                              int B, int H, int D, int P, int window, hipStream_t s) {
   RVC_CHECK(D >= 1 && D <= 128, "relpos_attention: head dim must be in [1,128]");
   RVC_CHECK(window >= 0 && window <= kMaxWindow, "relpos_attention: window must be in [0,15]");
+  RVC_CHECK((emb_k == nullptr) == (emb_v == nullptr), "relpos_attention: emb_k and emb_v go together");
   RVC_CHECK(P >= 1 && B >= 1 && H >= 1, "relpos_attention: invalid shape");
   const int KS = relpos_attention_splits(B, H, P);
   RVC_CHECK(KS == 1 || scratch != nullptr, "relpos_attention: scratch buffer required");

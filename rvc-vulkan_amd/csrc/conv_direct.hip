@@ -19,6 +19,7 @@ __device__ __forceinline__ float act_out(float v, int act, float slope) {
   if (act == ACT_LEAKY) return v >= 0.f ? v : v * slope;
   if (act == ACT_TANH) return tanhf(v);
   if (act == ACT_RELU) return fmaxf(v, 0.f);
+  if (act == ACT_GELU) return gelu_as(v);
   return v;
 }
 

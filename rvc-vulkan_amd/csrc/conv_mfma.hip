@@ -1,6 +1,6 @@
 // Implicit-GEMM conv1d on CDNA4 fp32 matrix cores (v_mfma_f32_32x32x2_f32).
 //
-// out[b][co][i] = sum_{ci,k} W[k][ci][co] * act(x[b][ci][i + in_off + k*dil])
+// out[b][co][i] = sum_{ci,k} W[k][ci][co] * act(x[b][ci][i*S + in_off + k*dil])
 // viewed as a GEMM with M = C_out, N = output positions and a reduction over
 // (ci, k).  One workgroup owns a BM x BN output tile.  For each chunk of
 // BK*SK input channels it stages, in LDS,
@@ -22,7 +22,7 @@
 //   row = (r%4) + 4*(l/32) + 8*(r/4), col = l%32.
 //
 // The fused epilogue adds bias (and an optional second per-channel term),
-// an optional residual, applies leaky-ReLU / ReLU / tanh and combines into
+// an optional residual, applies leaky-ReLU / ReLU / tanh / GELU and combines into
 // the output (store, accumulate, or accumulate-then-divide).  Output position
 // i is written at i*out_step + out_off, which lets one phase of a polyphase
 // ConvTranspose1d use the same kernel.  A launch may carry up to
@@ -43,10 +43,13 @@ __device__ __forceinline__ float apply_act(float v, int act, float slope) {
   if (act == ACT_LEAKY) return v >= 0.f ? v : v * slope;
   if (act == ACT_TANH) return tanhf(v);
   if (act == ACT_RELU) return fmaxf(v, 0.f);
+  if (act == ACT_GELU) return gelu_as(v);
   return v;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int SK>
+// S: input stride (output i reads inputs from i*S), a template parameter so
+// the staged window and the B-operand addressing fold it at compile time.
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1>
 struct Cfg {
   static constexpr int NWM = BM / WM;
   static constexpr int NWN = BN / WN;
@@ -55,21 +58,21 @@ struct Cfg {
   static constexpr int TM = WM / 32;
   static constexpr int TN = WN / 32;
   static constexpr int BKT = BK * SK;
-  static constexpr int XWMAX = BN + kConvHaloMax;
+  static constexpr int XWMAX = BN * S + kConvHaloMax;
   static constexpr int XPT = (BKT * XWMAX + NT - 1) / NT;
   static constexpr int W4ROW = BM / 4;
   static constexpr int WPT = (kConvTapsMax * BKT * W4ROW + NT - 1) / NT;
   static size_t lds_bytes(int K, int dil) {
-    const int XW = BN + (K > 0 ? (K - 1) * dil : 0);
+    const int XW = BN * S + (K > 0 ? (K - 1) * dil : 0);
     const size_t stage = sizeof(float) * ((size_t)BKT * XW + (size_t)K * BKT * BM);
     const size_t red = SK > 1 ? sizeof(float) * (size_t)(SK - 1) * NWM * NWN * TM * TN * 16 * 64 : 0;
     return stage > red ? stage : red;
   }
 };
 
-template <int BM, int BN, int WM, int WN, int BK, int SK>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_kernel(ConvLaunch a) {
-  using C = Cfg<BM, BN, WM, WN, BK, SK>;
+  using C = Cfg<BM, BN, WM, WN, BK, SK, S>;
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = C::BKT;
   constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
   static_assert(BK % 2 == 0 && BKT % 4 == 0, "channel chunk must be a multiple of 4");
@@ -82,7 +85,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
   const int co0 = blockIdx.y * BM;
   const int K = G.K;
   const int dil = G.dil;
-  const int XW = BN + (K > 0 ? (K - 1) * dil : 0);
+  const int XW = BN * S + (K > 0 ? (K - 1) * dil : 0);
 
   extern __shared__ float smem[];
   float* xs = smem;             // [BKT][XW]
@@ -111,7 +114,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
   float4 wreg[WPT];
   const int nx = BKT * XW;
   const int nw4 = K * BKT * W4ROW;
-  const int tbase = i0 + G.in_off;
+  const int tbase = i0 * S + G.in_off;
 
   auto gload = [&](int ci0) {
 #pragma unroll
@@ -164,7 +167,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
       if (c + 1 < nchunk) gload((c + 1) * BKT);
       for (int k = 0; k < K; ++k) {
         const float* wk_ = ws + (k * BKT + wk * BK) * BM + wm * WM + l32;
-        const float* xk = xs + wk * BK * XW + wn * WN + l32 + k * dil;
+        const float* xk = xs + wk * BK * XW + (wn * WN + l32) * S + k * dil;
 #pragma unroll
         for (int q = 0; q < BK / 2; ++q) {
           const int r = 2 * q + half;
@@ -172,7 +175,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
 #pragma unroll
           for (int m = 0; m < TM; ++m) av[m] = wk_[r * BM + m * 32];
 #pragma unroll
-          for (int n = 0; n < TN; ++n) bv[n] = xk[r * XW + n * 32];
+          for (int n = 0; n < TN; ++n) bv[n] = xk[r * XW + n * 32 * S];
 #pragma unroll
           for (int m = 0; m < TM; ++m)
 #pragma unroll
@@ -252,14 +255,14 @@ int max_n_out(const ConvLaunch& a) {
   return n;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int SK>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1>
 bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
-  using C = Cfg<BM, BN, WM, WN, BK, SK>;
+  using C = Cfg<BM, BN, WM, WN, BK, SK, S>;
   size_t lds = 0;
   for (int g = 0; g < a.n_groups; ++g) lds = std::max(lds, C::lds_bytes(a.g[g].K, a.g[g].dil));
   if (lds > kLdsLimit) return false;
   dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B);
-  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK>), grid, dim3(C::NT), lds, s, a);
+  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S>), grid, dim3(C::NT), lds, s, a);
   check_launch("conv1d_mfma");
   return true;
 }
@@ -283,9 +286,12 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   RVC_CHECK(a.n_groups >= 1 && a.n_groups <= kMaxConvGroups, "conv1d_mfma: bad group count");
   RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.B >= 1 && a.w_ld >= a.C_out && a.w_ld % 4 == 0,
             "conv1d_mfma: invalid shape");
+  const int step = a.g[0].in_step <= 1 ? 1 : a.g[0].in_step;
+  RVC_CHECK(step == 1 || step == 2, "conv1d_mfma: input stride must be 1 or 2");
   for (int g = 0; g < a.n_groups; ++g) {
     RVC_CHECK(a.g[g].n_out >= 0 && conv1d_mfma_supported(a.g[g].K, a.g[g].dil),
               "conv1d_mfma: taps / dilation outside the MFMA path");
+    RVC_CHECK((a.g[g].in_step <= 1 ? 1 : a.g[g].in_step) == step, "conv1d_mfma: groups must share the input stride");
     RVC_CHECK((reinterpret_cast<uintptr_t>(a.g[g].w) & 15) == 0, "conv1d_mfma: weights must be 16-byte aligned");
   }
   if (max_n_out(a) == 0) return;
@@ -297,6 +303,15 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   // 64 x 128 tiles).
   const long long want = 384;
   bool ok = false;
+  if (step == 2) {
+    // strided convolutions (the HuBERT feature extractor)
+    if (a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)
+      ok = launch_cfg<64, 128, 32, 64, 16, 1, 2>(a, s) || launch_cfg<64, 128, 32, 64, 8, 1, 2>(a, s);
+    if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 64) >= want) ok = launch_cfg<64, 64, 32, 32, 16, 1, 2>(a, s);
+    if (!ok) ok = launch_cfg<32, 64, 32, 32, 8, 4, 2>(a, s) || launch_cfg<32, 64, 32, 32, 4, 4, 2>(a, s);
+    RVC_CHECK(ok, "conv1d_mfma: no tile configuration fits the LDS budget");
+    return;
+  }
   if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)
     ok = launch_cfg<64, 128, 32, 64, 16, 1>(a, s) || launch_cfg<64, 128, 32, 64, 8, 1>(a, s);

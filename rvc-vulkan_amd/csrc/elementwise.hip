@@ -50,6 +50,11 @@ __global__ void mul_kernel(float* c, const float* a, const float* b, long long n
 __global__ void fill_kernel(float* a, long long n, float v) {
   GRID_STRIDE(i, n) a[i] = v;
 }
+// out = a + gelu(p)   (HuBERT encoder entry: h + pos_conv_embed(h),
+// runtime/models/hubert.py:855-857, :940)
+__global__ void add_gelu_kernel(float* o, const float* a, const float* p, long long n) {
+  GRID_STRIDE(i, n) o[i] = a[i] + gelu_as(p[i]);
+}
 __global__ void avg3_kernel(float* o, const float* a, const float* b, const float* c, long long n) {
   GRID_STRIDE(i, n) o[i] = ((a[i] + b[i]) + c[i]) / 3.0f;
 }
@@ -310,6 +315,12 @@ void launch_fill(float* a, long long n, float v, hipStream_t s) {
   hipLaunchKernelGGL(fill_kernel, dim3(capped_grid(n)), dim3(256), 0, s, a, n, v);
   check_launch("fill");
 }
+void launch_add_gelu(float* out, const float* a, const float* p, long long n, hipStream_t s) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(add_gelu_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, p, n);
+  check_launch("add_gelu");
+}
+
 void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s) {
   if (n <= 0) return;
   hipLaunchKernelGGL(avg3_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, b, c, n);

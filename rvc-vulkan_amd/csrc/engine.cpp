@@ -107,12 +107,13 @@ float bits_to_f32(long long v) {
 
 // A one-group MFMA launch over x [B][C_in][L] -> out [B][C_out][n_out].
 ConvLaunch one_conv(const float* x, long long C_in, long long L, const float* packed, const float* bias, float* out,
-                    long long C_out, long long n_out, long long B, long long K, long long dil, long long pad_l) {
+                    long long C_out, long long n_out, long long B, long long K, long long dil, long long pad_l,
+                    long long stride = 1) {
   ConvLaunch a{};
   a.n_groups = 1;
   ConvGroup& g = a.g[0];
   g.x = x; g.w = packed; g.bias = bias; g.res = nullptr; g.out = out;
-  g.K = (int)K; g.dil = (int)dil; g.in_off = (int)-pad_l; g.out_step = 1; g.out_off = 0;
+  g.K = (int)K; g.dil = (int)dil; g.in_off = (int)-pad_l; g.in_step = (int)stride; g.out_step = 1; g.out_off = 0;
   g.n_out = (int)n_out; g.combine = COMB_STORE;
   a.xb = C_in * L; a.xc = L; a.ob = C_out * n_out; a.oc = n_out;
   a.C_in = (int)C_in; a.C_out = (int)C_out; a.w_ld = packed_ld((int)C_out); a.L_in = (int)L; a.B = (int)B;
@@ -132,10 +133,10 @@ void op_conv1d(Engine& e, long long x, long long w, long long b, long long out, 
   const float* wp = e.fptr(w, C_out * C_in * K, "conv1d w");
   const float* bp = b ? e.fptr(b, C_out, "conv1d bias") : nullptr;
   float* op = e.fptr(out, B * C_out * n_out, "conv1d out");
-  if (stride == 1 && conv1d_mfma_supported((int)K, (int)dil)) {
+  if ((stride == 1 || stride == 2) && conv1d_mfma_supported((int)K, (int)dil)) {
     float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * packed_ld((int)C_out) * C_in * K));
     launch_pack_conv_weight(wp, packed, (int)C_out, (int)C_in, (int)K, e.stream);
-    launch_conv1d_mfma(one_conv(xp, C_in, L, packed, bp, op, C_out, n_out, B, K, dil, pad_l), e.stream);
+    launch_conv1d_mfma(one_conv(xp, C_in, L, packed, bp, op, C_out, n_out, B, K, dil, pad_l, stride), e.stream);
   } else {
     DirectConvArgs a{};
     a.x = xp; a.xb = C_in * L; a.xc = L;

@@ -42,7 +42,23 @@ void check_launch(const char* what);
 // ---------------------------------------------------------------- conv args
 // Activation applied while loading an input tile (prologue) or before the
 // combine step of the epilogue.
-enum Act : int { ACT_NONE = 0, ACT_LEAKY = 1, ACT_TANH = 2, ACT_RELU = 3 };
+enum Act : int { ACT_NONE = 0, ACT_LEAKY = 1, ACT_TANH = 2, ACT_RELU = 3, ACT_GELU = 4 };
+
+// GELU with erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), the
+// formula and float32 operation order of the reference's numpy gelu_erf
+// (runtime/models/hubert.py:194-202, :222-241): u = x / sqrt 2,
+// erf(u) = sign(u) (1 - poly(t) t exp(-u^2)) with t = 1 / (1 + p |u|).
+__device__ inline float gelu_as(float x) {
+#pragma clang fp contract(off)
+  const float u = x * 0.7071067811865476f;
+  const float au = fabsf(u);
+  const float t = 1.0f / (1.0f + 0.3275911f * au);
+  const float poly = ((((1.061405429f * t + -1.453152027f) * t) + 1.421413741f) * t + -0.284496736f) * t +
+                     0.254829592f;
+  const float y = 1.0f - poly * t * expf(-au * au);
+  const float e = u > 0.f ? y : (u < 0.f ? -y : 0.f);
+  return 0.5f * x * (1.0f + e);
+}
 
 // How the epilogue value v = act((acc + bias [+ bias2]) [+ res]) lands in out.
 enum Combine : int {
@@ -54,7 +70,7 @@ enum Combine : int {
 // MFMA fast path bounds: taps per conv and the input halo (K-1)*dil.
 constexpr int kConvTapsMax = 11;
 constexpr int kConvHaloMax = 64;
-constexpr int kMaxConvGroups = 12;
+constexpr int kMaxConvGroups = 16;
 
 // One convolution of a grouped MFMA launch (fields that differ per group).
 struct ConvGroup {
@@ -64,7 +80,8 @@ struct ConvGroup {
   const float* res;   // residual, indexed like out, or null
   float* out;
   int K, dil;
-  int in_off;         // input index of output i, tap k: i + in_off + k * dil
+  int in_off;         // input index of output i, tap k: i * in_step + in_off + k * dil
+  int in_step;        // input stride (0 or 1: stride 1; 2 supported)
   int out_step;       // output element index = i * out_step + out_off
   int out_off;
   int n_out;
@@ -88,8 +105,8 @@ struct ConvLaunch {
   float div;
 };
 
-// MFMA implicit-GEMM conv1d (stride 1), K <= kConvTapsMax and
-// (K-1)*dil <= kConvHaloMax.
+// MFMA implicit-GEMM conv1d (input stride 1 or 2, the same for every group
+// of a launch), K <= kConvTapsMax and (K-1)*dil <= kConvHaloMax.
 bool conv1d_mfma_supported(int K, int dil);
 void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s);
 
@@ -152,6 +169,8 @@ void launch_mul_inplace(float* a, const float* b, long long n, hipStream_t s);
 void launch_add(float* c, const float* a, const float* b, long long n, hipStream_t s);
 void launch_mul(float* c, const float* a, const float* b, long long n, hipStream_t s);
 void launch_fill(float* a, long long n, float v, hipStream_t s);
+// out = a + gelu(p)
+void launch_add_gelu(float* out, const float* a, const float* p, long long n, hipStream_t s);
 // out = ((a + b) + c) / 3   (the ResBlock average, runtime/models/vits.py:2225-2227)
 void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s);
 // out[i, :] = table[ids[i], :], ids int32 with negative wrap.
@@ -198,9 +217,13 @@ void launch_layernorm_rows(const float* x, const float* g, const float* b, float
 void launch_layernorm_cols(const float* x, const float* g, const float* b, float* out, int B, int C,
                            int L, float eps, hipStream_t s);
 void launch_softmax_rows(const float* x, float* out, long long rows, int cols, hipStream_t s);
+// One-channel-per-group GroupNorm over L of x[B][C][L], affine per channel, then act.
+void launch_groupnorm_rows_act(const float* x, const float* g, const float* b, float* out, int B, int C, long long L,
+                               float eps, int act, hipStream_t s);
 
 // ---------------------------------------------------------------- attention
-// Windowed relative-position attention, all heads.
+// Windowed relative-position attention, all heads (emb_k = emb_v = null:
+// plain attention).
 // qkv[b][3*H*D][P] (q, k, v stacked), emb_k/emb_v [2w+1][D], out[b][H*D][P];
 // scratch holds relpos_attention_scratch_floats(B,H,D,P) floats (may be
 // null when that is 0).

@@ -56,6 +56,37 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const float* x, con
   for (int c = threadIdx.x; c < cols; c += blockDim.x) orow[c] = (xr[c] - mean) / den * g[c] + b[c];
 }
 
+// GroupNorm with one channel per group on [B][C][L] (the normalisation runs
+// over L for each (b, c)), two-pass in float64 like the row LayerNorm, then
+// the per-channel affine and an activation:
+//   out = act((x - mean) / sqrt(var + eps) * g[c] + b[c])
+// (runtime/nn.py:415-436 with num_groups == C, then gelu_erf for HuBERT's
+// first feature-extractor layer, runtime/models/hubert.py:686-692).
+__global__ __launch_bounds__(256) void groupnorm_rows_act_kernel(const float* x, const float* g, const float* b,
+                                                                 float* out, int C, long long L, float eps, int act) {
+  __shared__ double sh[256 / 64];
+  const long long row = blockIdx.x;
+  const int c = (int)(row % C);
+  const float* xr = x + row * L;
+  float* orow = out + row * L;
+  double s = 0.0;
+  for (long long i = threadIdx.x; i < L; i += blockDim.x) s += xr[i];
+  const float mean = (float)(block_sum_d(s, sh) / (double)L);
+  double v = 0.0;
+  for (long long i = threadIdx.x; i < L; i += blockDim.x) {
+    const float d = xr[i] - mean;
+    v += (double)d * d;
+  }
+  const float var = (float)(block_sum_d(v, sh) / (double)L);
+  const float den = sqrtf(var + eps);
+  const float gc = g[c], bc = b[c];
+  for (long long i = threadIdx.x; i < L; i += blockDim.x) {
+    float y = (xr[i] - mean) / den * gc + bc;
+    if (act == ACT_GELU) y = gelu_as(y);
+    orow[i] = y;
+  }
+}
+
 // Channel-major [B][C][L]: normalise over C for each (b, t).  A workgroup
 // owns LN_COLS consecutive columns; its LN_GRP thread groups split the
 // channels (coalesced reads along t) and combine partial sums in LDS.
@@ -141,6 +172,14 @@ void launch_layernorm_cols(const float* x, const float* g, const float* b, float
   dim3 grid((L + LN_COLS - 1) / LN_COLS, B);
   hipLaunchKernelGGL(layernorm_cols_kernel, grid, dim3(LN_COLS * LN_GRP), 0, s, x, g, b, out, C, L, eps);
   check_launch("layernorm_cols");
+}
+
+void launch_groupnorm_rows_act(const float* x, const float* g, const float* b, float* out, int B, int C, long long L,
+                               float eps, int act, hipStream_t s) {
+  if (B <= 0 || C <= 0 || L <= 0) return;
+  hipLaunchKernelGGL(groupnorm_rows_act_kernel, dim3((unsigned)((long long)B * C)), dim3(256), 0, s, x, g, b, out, C,
+                     L, eps, act);
+  check_launch("groupnorm_rows_act");
 }
 
 void launch_softmax_rows(const float* x, float* out, long long rows, int cols, hipStream_t s) {

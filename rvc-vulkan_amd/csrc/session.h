@@ -1,0 +1,209 @@
+// Shared machinery of the device-resident sessions (rvc_synth_*, rvc_hubert_*):
+// checkpoint tensors staged on the host by key until finalize, packed device
+// weights owned by the session, a named workspace of device buffers reused
+// across calls, and per-launch HIP-event timing selected by a tag prefix.
+#pragma once
+
+#include <algorithm>
+#include <cstring>
+
+#include "engine.h"
+
+namespace rvc {
+
+struct HostT {
+  std::vector<float> data;
+  std::vector<long long> shape;
+};
+
+struct SessionBase {
+  Engine* eng = nullptr;
+  std::map<std::string, HostT> host;
+  bool ready = false;
+  std::vector<void*> owned;
+  std::map<std::string, std::pair<float*, size_t>> ws;
+
+  // timing
+  std::string tag;
+  struct Ev {
+    hipEvent_t a, b;
+    double flops, bytes;
+  };
+  std::vector<Ev> pending;
+  std::vector<hipEvent_t> pool;
+  double t_ms = 0, t_flops = 0, t_bytes = 0;
+  long long t_n = 0;
+
+  virtual ~SessionBase() {
+    if (eng && eng->stream) (void)hipStreamSynchronize(eng->stream);
+    for (void* p : owned) (void)hipFree(p);
+    for (auto& kv : ws) (void)hipFree(kv.second.first);
+    for (auto& e : pending) pool.push_back(e.a), pool.push_back(e.b);
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+  }
+
+  // -------------------------------------------------------------- host weights
+  void set_weight(const char* key, const float* data, const int64_t* shape, int ndim) {
+    RVC_CHECK(!ready, "session already finalized");
+    RVC_CHECK(key && data && shape && ndim >= 1 && ndim <= 8, "set_weight: invalid arguments");
+    HostT t;
+    long long n = 1;
+    for (int i = 0; i < ndim; ++i) {
+      RVC_CHECK(shape[i] >= 0, "set_weight: negative dimension");
+      t.shape.push_back(shape[i]);
+      n *= shape[i];
+    }
+    t.data.assign(data, data + n);
+    host[key] = std::move(t);
+  }
+  const HostT& W(const std::string& k) const {
+    auto it = host.find(k);
+    if (it == host.end()) throw Error("missing weight: " + k);
+    return it->second;
+  }
+  bool has(const std::string& k) const { return host.count(k) != 0; }
+
+  static void check_shape(const std::string& k, const std::vector<long long>& got, std::vector<long long> want) {
+    if (got != want) {
+      std::string g, wv;
+      for (auto x : got) g += std::to_string(x) + ",";
+      for (auto x : want) wv += std::to_string(x) + ",";
+      throw Error("weight " + k + " has shape [" + g + "], expected [" + wv + "]");
+    }
+  }
+
+  // [C_out][C_in][K] -> [K][C_in][packed_ld(C_out)], pad columns zero
+  static std::vector<float> pack(const std::vector<float>& w, long long C_out, long long C_in, long long K) {
+    const long long ld = packed_ld((int)C_out);
+    std::vector<float> o((size_t)(K * C_in * ld), 0.f);
+    for (long long co = 0; co < C_out; ++co)
+      for (long long ci = 0; ci < C_in; ++ci)
+        for (long long k = 0; k < K; ++k) o[(k * C_in + ci) * ld + co] = w[(co * C_in + ci) * K + k];
+    return o;
+  }
+
+  float* upload(const std::vector<float>& v) {
+    void* p = nullptr;
+    RVC_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 1) * sizeof(float)));
+    owned.push_back(p);
+    if (!v.empty()) RVC_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+    return static_cast<float*>(p);
+  }
+  float* upload_key(const std::string& k) { return upload(W(k).data); }
+  float* upload_vec(const std::string& k, long long n) {
+    const HostT& t = W(k);
+    RVC_CHECK((long long)t.data.size() == n, "weight " + k + " must hold " + std::to_string(n) + " values");
+    return upload(t.data);
+  }
+
+  // -------------------------------------------------------------- workspace
+  float* buf(const std::string& name, size_t n) {
+    auto it = ws.find(name);
+    if (it != ws.end() && it->second.second >= n) return it->second.first;
+    RVC_HIP(hipStreamSynchronize(eng->stream));
+    if (it != ws.end()) {
+      RVC_HIP(hipFree(it->second.first));
+      ws.erase(it);
+    }
+    void* p = nullptr;
+    RVC_HIP(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(float)));
+    ws[name] = {static_cast<float*>(p), n};
+    return static_cast<float*>(p);
+  }
+  void read(const std::string& nm, float* dst, long long n) {
+    auto it = ws.find(nm);
+    RVC_CHECK(it != ws.end(), "read: no intermediate named " + nm);
+    RVC_CHECK((size_t)n <= it->second.second, "read: " + nm + " holds fewer values");
+    RVC_HIP(hipMemcpyAsync(dst, it->second.first, sizeof(float) * n, hipMemcpyDeviceToHost, eng->stream));
+    RVC_HIP(hipStreamSynchronize(eng->stream));
+  }
+
+  // -------------------------------------------------------------- timing
+  bool timed(const char* t) const { return !tag.empty() && std::strncmp(t, tag.c_str(), tag.size()) == 0; }
+  hipEvent_t ev() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e;
+    RVC_HIP(hipEventCreate(&e));
+    return e;
+  }
+  template <class Fn>
+  void run(const char* t, double flops, double bytes, Fn&& fn) {
+    if (!timed(t)) {
+      fn();
+      return;
+    }
+    Ev e{ev(), ev(), flops, bytes};
+    RVC_HIP(hipEventRecord(e.a, eng->stream));
+    fn();
+    RVC_HIP(hipEventRecord(e.b, eng->stream));
+    pending.push_back(e);
+  }
+  void collect_timing() {
+    for (auto& e : pending) {
+      float ms = 0;
+      RVC_HIP(hipEventElapsedTime(&ms, e.a, e.b));
+      t_ms += ms;
+      t_flops += e.flops;
+      t_bytes += e.bytes;
+      ++t_n;
+      pool.push_back(e.a);
+      pool.push_back(e.b);
+    }
+    pending.clear();
+  }
+  void set_timing(const char* t) {
+    tag = t ? t : "";
+    t_ms = t_flops = t_bytes = 0;
+    t_n = 0;
+  }
+
+  // -------------------------------------------------------------- conv helpers
+  // One conv x [B][C_in][L_in] -> out [B][C_out][n_out]: output i reads
+  // x[i*stride - pad + k*dil].
+  static ConvLaunch cargs(const float* x, long long xb, long long xc, const float* w, const float* bias, float* out,
+                          long long ob, long long oc, int B, int C_in, int C_out, int L_in, int n_out, int K, int dil,
+                          int pad, int stride = 1) {
+    ConvLaunch a{};
+    a.n_groups = 1;
+    ConvGroup& g = a.g[0];
+    g.x = x; g.w = w; g.bias = bias; g.res = nullptr; g.out = out;
+    g.K = K; g.dil = dil; g.in_off = -pad; g.in_step = stride; g.out_step = 1; g.out_off = 0; g.n_out = n_out;
+    g.combine = COMB_STORE;
+    a.xb = xb; a.xc = xc; a.ob = ob; a.oc = oc;
+    a.C_in = C_in; a.C_out = C_out; a.w_ld = packed_ld(C_out); a.L_in = L_in; a.B = B;
+    a.div = 1.f;
+    return a;
+  }
+  // stride-1 conv with output length == input length L ("same" padding)
+  static ConvLaunch cargs_same(const float* x, long long xb, long long xc, const float* w, const float* bias,
+                               float* out, long long ob, long long oc, int B, int C_in, int C_out, int L, int K,
+                               int dil, int pad) {
+    return cargs(x, xb, xc, w, bias, out, ob, oc, B, C_in, C_out, L, L, K, dil, pad);
+  }
+  // 1x1 conv: x [B][C_in][L] -> out [B][C_out][L]
+  static ConvLaunch c1x1(const float* x, long long xb, const float* w, const float* b, float* out, int B, int C_in,
+                         int C_out, int L) {
+    return cargs(x, xb, L, w, b, out, (long long)C_out * L, L, B, C_in, C_out, L, L, 1, 1, 0);
+  }
+  // Algorithmic FLOPs / bytes of a launch (each group's input, output,
+  // weights, residual, and the read-back of an accumulating combine).
+  void conv(const char* t, const ConvLaunch& a) {
+    double mac = 0, bytes = 0;
+    for (int i = 0; i < a.n_groups; ++i) {
+      const ConvGroup& g = a.g[i];
+      const double outs = (double)a.B * a.C_out * g.n_out;
+      mac += outs * a.C_in * g.K;
+      bytes += 4.0 * (outs + (double)a.C_out * a.C_in * g.K);
+      if (i == 0 || g.x != a.g[i - 1].x) bytes += 4.0 * (double)a.B * a.C_in * a.L_in;
+      if (g.res) bytes += 4.0 * outs;
+      if (g.combine != COMB_STORE) bytes += 4.0 * outs;
+    }
+    run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
+  }
+};
+
+}  // namespace rvc

@@ -24,19 +24,11 @@
 #include <cstring>
 
 #include "../../include/rvc_hip.h"
-#include "engine.h"
+#include "session.h"
 
 namespace rvc {
 
-struct HostT {
-  std::vector<float> data;
-  std::vector<long long> shape;
-};
-
-struct Synth {
-  Engine* eng = nullptr;
-  std::map<std::string, HostT> host;
-  bool ready = false;
+struct Synth : SessionBase {
 
   // ---- geometry (VitsConfig, runtime/models/vits.py:166-268) ----
   int phone_dim = 0, H = 0, F = 0, n_layers = 0, heads = 0, kc = 0, gin = 0, n_spk = 0;
@@ -45,7 +37,6 @@ struct Synth {
   std::vector<int> rates, kernels, chans, noise_k, noise_s;
 
   // ---- device weights ----
-  std::vector<void*> owned;
   float *emb_phone_w = nullptr, *emb_phone_b = nullptr, *emb_pitch = nullptr, *emb_g = nullptr;
   struct EncL {
     float *wqkv, *bqkv, *wo, *bo, *ek, *ev, *g1, *b1, *w1, *bf1, *w2, *bf2, *g2, *b2;
@@ -70,37 +61,10 @@ struct Synth {
   std::vector<StageW> stages;
 
   // ---- workspace ----
-  std::map<std::string, std::pair<float*, size_t>> ws;
   bool keep_stages = false;
   std::string z_name = "z_p";  // workspace buffer holding the last flow output
 
-  // ---- timing ----
-  std::string tag;
-  struct Ev {
-    hipEvent_t a, b;
-    double flops, bytes;
-  };
-  std::vector<Ev> pending;
-  std::vector<hipEvent_t> pool;
-  double t_ms = 0, t_flops = 0, t_bytes = 0;
-  long long t_n = 0;
-
-  ~Synth() {
-    if (eng && eng->stream) (void)hipStreamSynchronize(eng->stream);
-    for (void* p : owned) (void)hipFree(p);
-    for (auto& kv : ws) (void)hipFree(kv.second.first);
-    for (auto& e : pending) pool.push_back(e.a), pool.push_back(e.b);
-    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
-  }
-
   // -------------------------------------------------------------- weights
-  const HostT& W(const std::string& k) const {
-    auto it = host.find(k);
-    if (it == host.end()) throw Error("missing weight: " + k);
-    return it->second;
-  }
-  bool has(const std::string& k) const { return host.count(k) != 0; }
-
   std::vector<float> deweight(const std::string& base) const {
     // W = v * (g / max(||v||, 1e-12)), norm over all dims but 0
     // (runtime/models/vits.py:416-442)
@@ -121,25 +85,6 @@ struct Synth {
     return out;
   }
 
-  // [C_out][C_in][K] -> [K][C_in][packed_ld(C_out)], pad columns zero
-  static std::vector<float> pack(const std::vector<float>& w, long long C_out, long long C_in, long long K) {
-    const long long ld = packed_ld((int)C_out);
-    std::vector<float> o((size_t)(K * C_in * ld), 0.f);
-    for (long long co = 0; co < C_out; ++co)
-      for (long long ci = 0; ci < C_in; ++ci)
-        for (long long k = 0; k < K; ++k) o[(k * C_in + ci) * ld + co] = w[(co * C_in + ci) * K + k];
-    return o;
-  }
-
-  float* upload(const std::vector<float>& v) {
-    void* p = nullptr;
-    RVC_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 1) * sizeof(float)));
-    owned.push_back(p);
-    if (!v.empty()) RVC_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
-    return static_cast<float*>(p);
-  }
-  float* upload_key(const std::string& k) { return upload(W(k).data); }
-
   float* upload_conv(const std::string& key, long long C_out, long long C_in, long long K, bool wn) {
     std::vector<float> w;
     if (wn) {
@@ -152,21 +97,6 @@ struct Synth {
       w = t.data;
     }
     return upload(pack(w, C_out, C_in, K));
-  }
-
-  static void check_shape(const std::string& k, const std::vector<long long>& got, std::vector<long long> want) {
-    if (got != want) {
-      std::string g, wv;
-      for (auto x : got) g += std::to_string(x) + ",";
-      for (auto x : want) wv += std::to_string(x) + ",";
-      throw Error("weight " + k + " has shape [" + g + "], expected [" + wv + "]");
-    }
-  }
-
-  float* upload_vec(const std::string& k, long long n) {
-    const HostT& t = W(k);
-    RVC_CHECK((long long)t.data.size() == n, "weight " + k + " must hold " + std::to_string(n) + " values");
-    return upload(t.data);
   }
 
   void finalize(int sr_, const std::vector<int>& rates_, const std::vector<int>& kernels_) {
@@ -329,21 +259,6 @@ struct Synth {
     ready = true;
   }
 
-  // -------------------------------------------------------------- workspace
-  float* buf(const std::string& name, size_t n) {
-    auto it = ws.find(name);
-    if (it != ws.end() && it->second.second >= n) return it->second.first;
-    RVC_HIP(hipStreamSynchronize(eng->stream));
-    if (it != ws.end()) {
-      RVC_HIP(hipFree(it->second.first));
-      ws.erase(it);
-    }
-    void* p = nullptr;
-    RVC_HIP(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(float)));
-    ws[name] = {static_cast<float*>(p), n};
-    return static_cast<float*>(p);
-  }
-
   // stage lengths and the decoder ping-pong capacity for P frames
   size_t dec_cap(int P) const {
     size_t cap = (size_t)U * P;
@@ -353,76 +268,6 @@ struct Synth {
       cap = std::max(cap, (size_t)(chans[i] * L));
     }
     return cap;
-  }
-
-  // -------------------------------------------------------------- timing
-  bool timed(const char* t) const { return !tag.empty() && std::strncmp(t, tag.c_str(), tag.size()) == 0; }
-  hipEvent_t ev() {
-    if (!pool.empty()) {
-      hipEvent_t e = pool.back();
-      pool.pop_back();
-      return e;
-    }
-    hipEvent_t e;
-    RVC_HIP(hipEventCreate(&e));
-    return e;
-  }
-  template <class Fn>
-  void run(const char* t, double flops, double bytes, Fn&& fn) {
-    if (!timed(t)) {
-      fn();
-      return;
-    }
-    Ev e{ev(), ev(), flops, bytes};
-    RVC_HIP(hipEventRecord(e.a, eng->stream));
-    fn();
-    RVC_HIP(hipEventRecord(e.b, eng->stream));
-    pending.push_back(e);
-  }
-  void collect_timing() {
-    for (auto& e : pending) {
-      float ms = 0;
-      RVC_HIP(hipEventElapsedTime(&ms, e.a, e.b));
-      t_ms += ms;
-      t_flops += e.flops;
-      t_bytes += e.bytes;
-      ++t_n;
-      pool.push_back(e.a);
-      pool.push_back(e.b);
-    }
-    pending.clear();
-  }
-
-  // -------------------------------------------------------------- conv helpers
-  // One stride-1 conv x [B][C_in][L] -> out [B][C_out][L] ("same" length).
-  ConvLaunch cargs(const float* x, long long xb, long long xc, const float* w, const float* bias, float* out,
-                   long long ob, long long oc, int B, int C_in, int C_out, int L, int K, int dil, int pad) {
-    ConvLaunch a{};
-    a.n_groups = 1;
-    ConvGroup& g = a.g[0];
-    g.x = x; g.w = w; g.bias = bias; g.res = nullptr; g.out = out;
-    g.K = K; g.dil = dil; g.in_off = -pad; g.out_step = 1; g.out_off = 0; g.n_out = L; g.combine = COMB_STORE;
-    a.xb = xb; a.xc = xc; a.ob = ob; a.oc = oc;
-    a.C_in = C_in; a.C_out = C_out; a.w_ld = packed_ld(C_out); a.L_in = L; a.B = B;
-    a.div = 1.f;
-    return a;
-  }
-  void conv(const char* t, const ConvLaunch& a) {
-    double mac = 0, bytes = 4.0 * (double)a.B * a.C_in * a.L_in;
-    for (int i = 0; i < a.n_groups; ++i) {
-      const ConvGroup& g = a.g[i];
-      const double outs = (double)a.B * a.C_out * g.n_out;
-      mac += outs * a.C_in * g.K;
-      bytes += 4.0 * (outs + (double)a.C_out * a.C_in * g.K);
-      if (g.res) bytes += 4.0 * outs;
-      if (g.combine != COMB_STORE) bytes += 4.0 * outs;
-    }
-    run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
-  }
-  // 1x1 conv: x [B][C_in][L] -> out [B][C_out][L]
-  ConvLaunch c1x1(const float* x, long long xb, const float* w, const float* b, float* out, int B, int C_in,
-                  int C_out, int L) {
-    return cargs(x, xb, L, w, b, out, (long long)C_out * L, L, B, C_in, C_out, L, 1, 1, 0);
   }
 
   // -------------------------------------------------------------- enc_p + flow
@@ -454,10 +299,10 @@ struct Synth {
       co.g[0].res = x; co.rb = HP; co.rc = P;
       conv("enc.o", co);
       run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g1, L.b1, xo, B, H, P, 1e-5f, s); });
-      ConvLaunch c1 = cargs(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
+      ConvLaunch c1 = cargs_same(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
       c1.out_act = ACT_RELU;
       conv("enc.ffn", c1);
-      ConvLaunch c2 = cargs(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
+      ConvLaunch c2 = cargs_same(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
       c2.g[0].res = xo; c2.rb = HP; c2.rc = P;
       conv("enc.ffn", c2);
       run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g2, L.b2, xo, B, H, P, 1e-5f, s); });
@@ -486,7 +331,7 @@ struct Synth {
       conv("flow.pre", c1x1(dst, HP, L.pre_w, L.pre_b, h, B, half, H, P));
       launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s);
       for (int i = 0; i < kWnLayers; ++i) {
-        conv("flow.in", cargs(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
+        conv("flow.in", cargs_same(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
                               (kWnKernel - 1) / 2));
         launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
         conv("flow.rs", c1x1(acts, HP, L.rs_w[i], L.rs_b[i], rs, B, H, L.rs_out[i], P));
@@ -522,7 +367,7 @@ struct Synth {
       Y[j] = buf("dY" + std::to_string(j), (size_t)B * cap);
     }
     float* pre = buf("dec_pre", (size_t)B * U * P);
-    ConvLaunch ca = cargs(z, zb, P, dpre_w, dpre_b, pre, (long long)U * P, P, B, H, U, P, 7, 1, 3);
+    ConvLaunch ca = cargs_same(z, zb, P, dpre_w, dpre_b, pre, (long long)U * P, P, B, H, U, P, 7, 1, 3);
     ca.bias2 = cv;
     ca.bias2b = U;
     conv("dec.pre", ca);
@@ -569,7 +414,7 @@ struct Synth {
       std::snprintf(tg, sizeof tg, "dec.rb.s%d", i);
       for (int gi = 0; gi < 3; ++gi) {
         const int d = ds[gi];
-        ConvLaunch c1 = cargs(nullptr, CL, Lo, nullptr, nullptr, nullptr, CL, Lo, B, C, C, Lo, 1, 1, 0);
+        ConvLaunch c1 = cargs_same(nullptr, CL, Lo, nullptr, nullptr, nullptr, CL, Lo, B, C, C, Lo, 1, 1, 0);
         ConvLaunch c2 = c1;
         c1.n_groups = c2.n_groups = 3;
         c1.in_act = ACT_LEAKY; c1.in_slope = 0.1f;
@@ -691,19 +536,7 @@ int32_t rvc_synth_destroy(int64_t sh) {
 }
 
 int32_t rvc_synth_set_weight(int64_t sh, const char* key, const float* data, const int64_t* shape, int32_t ndim) {
-  return sguard(sh, [&](Synth& s) {
-    RVC_CHECK(!s.ready, "synth session already finalized");
-    RVC_CHECK(key && data && shape && ndim >= 1 && ndim <= 8, "set_weight: invalid arguments");
-    HostT t;
-    long long n = 1;
-    for (int i = 0; i < ndim; ++i) {
-      RVC_CHECK(shape[i] >= 0, "set_weight: negative dimension");
-      t.shape.push_back(shape[i]);
-      n *= shape[i];
-    }
-    t.data.assign(data, data + n);
-    s.host[key] = std::move(t);
-  });
+  return sguard(sh, [&](Synth& s) { s.set_weight(key, data, shape, ndim); });
 }
 
 int32_t rvc_synth_finalize(int64_t sh, int64_t sr, const int64_t* rates, const int64_t* kernels, int32_t n_ups) {
@@ -816,12 +649,7 @@ int32_t rvc_synth_decode(int64_t sh, const float* z, const float* f0, const floa
 int32_t rvc_synth_read(int64_t sh, const char* name, float* dst, int64_t n) {
   return sguard(sh, [&](Synth& s) {
     RVC_CHECK(name && dst && n >= 0, "read: invalid arguments");
-    const std::string nm = std::strcmp(name, "z") == 0 ? s.z_name : std::string(name);
-    auto it = s.ws.find(nm);
-    RVC_CHECK(it != s.ws.end(), std::string("read: no intermediate named ") + name);
-    RVC_CHECK((size_t)n <= it->second.second, std::string("read: ") + name + " holds fewer values");
-    RVC_HIP(hipMemcpyAsync(dst, it->second.first, sizeof(float) * n, hipMemcpyDeviceToHost, s.eng->stream));
-    RVC_HIP(hipStreamSynchronize(s.eng->stream));
+    s.read(std::strcmp(name, "z") == 0 ? s.z_name : std::string(name), dst, n);
   });
 }
 
@@ -830,11 +658,7 @@ int32_t rvc_synth_set_debug(int64_t sh, int32_t keep_stages) {
 }
 
 int32_t rvc_synth_set_timing(int64_t sh, const char* tag) {
-  return sguard(sh, [&](Synth& s) {
-    s.tag = tag ? tag : "";
-    s.t_ms = s.t_flops = s.t_bytes = 0;
-    s.t_n = 0;
-  });
+  return sguard(sh, [&](Synth& s) { s.set_timing(tag); });
 }
 
 int32_t rvc_synth_get_timing(int64_t sh, double* total_ms, int64_t* launches, double* flops, double* bytes) {

@@ -90,6 +90,18 @@ SYMBOLS = {
     "rvc_synth_set_timing": (I32, [I64, CHARP]),
     "rvc_synth_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL),
                                    ctypes.POINTER(DBL)]),
+    "rvc_hubert_create": (I64, [I64]),
+    "rvc_hubert_destroy": (I32, [I64]),
+    "rvc_hubert_set_weight": (I32, [I64, CHARP, F32P, I64P, I32]),
+    "rvc_hubert_finalize": (I32, [I64]),
+    "rvc_hubert_frames": (I32, [I64, I64, I64P]),
+    "rvc_hubert_encode": (I32, [I64, F32P, I64, I64, I32, F32P]),
+    "rvc_hubert_encode_dev": (I32, [I64, I64, I64, I64, I32, I64]),
+    "rvc_hubert_read": (I32, [I64, CHARP, F32P, I64]),
+    "rvc_hubert_set_debug": (I32, [I64, I32]),
+    "rvc_hubert_set_timing": (I32, [I64, CHARP]),
+    "rvc_hubert_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL),
+                                    ctypes.POINTER(DBL)]),
 }
 
 

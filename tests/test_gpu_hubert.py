@@ -1,0 +1,103 @@
+# -*- coding: utf-8 -*-
+"""HuBERT-base encoder on the HIP backend (GPU) against the reference's own
+outputs (tests/golden/hubert_base.npz) and the numpy oracle
+(oracle/hubert_ref.py) on identical seeded inputs and random-init weights.
+
+Tolerance: per-stage relative L2 <= 1e-4 (the engine self-test's op measure,
+engine/test_ffi.py:103-105); the final hidden states are LayerNorm outputs of
+order one, compared at rel L2 <= 1e-4 and max-abs <= 1e-3.  At BASELINE
+config 3's full size (160 000 samples) the oracle comparison runs on a 2 s
+prefix-length input instead, and the full size is checked through shape,
+determinism and batch == per-chunk identity."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, rel_l2
+from oracle import hubert_ref as H
+from rvc_hip import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(os.path.join(GOLDEN, "hubert_base.npz"))
+
+
+@pytest.fixture(scope="module")
+def sd(golden):
+    w = syn.make_hubert_weights(syn.HUBERT_BASE, seed=int(golden["wseed"]))
+    assert syn.weights_digest(w) == str(golden["digest"])
+    return w
+
+
+@pytest.fixture(scope="module")
+def hub(sd):
+    from rvc_hip import _hip
+    from rvc_hip.hubert import HipHubert
+
+    assert _hip.has_so, _hip.so_load_error
+    return HipHubert(sd)
+
+
+@pytest.mark.parametrize("T", [1600, 4000])
+def test_golden_stages_and_outputs(golden, hub, T):
+    x = golden[f"T{T}_x"]
+    hub.set_debug(True)
+    v2 = hub.encode(x, version=2)
+    hub.set_debug(False)
+    L = v2.shape[1]
+    assert v2.shape == golden[f"T{T}_v2"].shape
+    feats = hub.read("feats", (1, 512, L)).transpose(0, 2, 1)
+    assert rel_l2(feats, golden[f"T{T}_feats"]) < TOL
+    proj = hub.read("proj", (1, 768, L)).transpose(0, 2, 1)
+    assert rel_l2(proj, golden[f"T{T}_proj"]) < TOL
+    entry = hub.read("entry", (1, 768, L)).transpose(0, 2, 1)
+    assert rel_l2(entry, golden[f"T{T}_entry"]) < TOL
+    layer1 = hub.read("layer1", (1, 768, L)).transpose(0, 2, 1)
+    assert rel_l2(layer1, golden[f"T{T}_layer1"]) < TOL
+    assert rel_l2(v2, golden[f"T{T}_v2"]) < TOL
+    assert np.abs(v2 - golden[f"T{T}_v2"]).max() < 1e-3
+    v1 = hub.encode(x, version=1)
+    assert v1.shape == golden[f"T{T}_v1"].shape
+    assert rel_l2(v1, golden[f"T{T}_v1"]) < TOL
+
+
+def test_two_seconds_vs_oracle(sd, hub):
+    x = syn.make_hubert_input(32000, seed=8)
+    got = hub.encode(x, version=2)
+    want = H.HubertRef(sd).encode(x, version=2)
+    assert got.shape == want.shape == (1, 99, 768)
+    assert rel_l2(got, want) < TOL
+    assert np.abs(got - want).max() < 1e-3
+
+
+def test_config3_full_size_properties(hub):
+    """10 s of 16 kHz audio -> [1, 499, 768]."""
+    x = syn.make_hubert_input(160000, seed=3)
+    a = hub.encode(x, version=2)
+    b = hub.encode(x, version=2)
+    assert a.shape == (1, 499, 768)
+    np.testing.assert_array_equal(a, b)
+    assert np.isfinite(a).all()
+    # post-LN rows: (x - mean)/std * gamma + beta, so every row has a spread of order one
+    assert 0.3 < float(a.std(axis=-1).mean()) < 3.0
+
+
+def test_batch_equals_per_chunk(hub):
+    xs = [syn.make_hubert_input(8000, seed=s) for s in (1, 2)]
+    both = hub.encode(np.concatenate(xs, axis=0), version=2)
+    for i, x in enumerate(xs):
+        np.testing.assert_array_equal(both[i:i + 1], hub.encode(x, version=2))
+
+
+def test_rejects_too_short_input(hub):
+    with pytest.raises(ValueError):
+        hub.encode(np.zeros((1, 300), np.float32))

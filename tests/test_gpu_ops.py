@@ -88,6 +88,28 @@ def test_conv1d_noise_conv_shapes(ops, C_out, k, s):
     assert rel_l2(got, nn.conv1d(x, w, b, stride=s, padding=s // 2)) < TOL
 
 
+@pytest.mark.parametrize("B,C,O,T,K,pl,pr,d", [
+    (1, 5, 70, 33, 3, 0, 0, 1),
+    (2, 17, 64, 200, 2, 0, 0, 1),
+    (1, 3, 40, 57, 5, 2, 1, 2),
+])
+def test_conv1d_stride2_small_vs_loops(ops, B, C, O, T, K, pl, pr, d):
+    """Stride-2 convolutions run on the MFMA kernel's strided variant."""
+    rng = np.random.default_rng(9)
+    x, w, b = _r(rng, B, C, T), _r(rng, O, C, K), _r(rng, O)
+    got = ops.conv1d(x, w, b, stride=2, padding=(pl, pr), dilation=d)
+    assert rel_l2(got, loops.conv1d(x, w, b, 2, pl, pr, d)) < TOL
+
+
+@pytest.mark.parametrize("T,K", [(2001, 3), (999, 2)])
+def test_conv1d_hubert_feature_shapes(ops, T, K):
+    """HuBERT feature-extractor layers: 512 -> 512, valid, stride 2."""
+    rng = np.random.default_rng(10)
+    x, w = _r(rng, 1, 512, T), _r(rng, 512, 512, K, scale=(2.0 / (512 * K)) ** 0.5)
+    got = ops.conv1d(x, w, None, stride=2)
+    assert rel_l2(got, nn.conv1d(x, w, None, stride=2)) < TOL
+
+
 @pytest.mark.parametrize("C_in,C_out,L,K,s,p,op,d", [
     (512, 256, 50, 16, 10, 3, 0, 1),
     (256, 128, 200, 16, 10, 3, 0, 1),
