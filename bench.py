@@ -1,7 +1,7 @@
 # -*- coding: utf-8 -*-
 """Benchmark: RVC v2 40k synthesis throughput on one MI355X.
 
-Workload ("config 2"): full synthesizer
+Default workload ("config 2"): full synthesizer
 enc_p + flow + GeneratorNSF, fp32, random-init weights, 10 s of 40 kHz audio
 (P = 1000 frames), batch 1.  One step = one ``rvc_synth_infer_dev`` call over
 inputs already resident in HBM (phone [1,1000,768], pitch, nsff0, sid, the
@@ -11,6 +11,11 @@ Prints ONE JSON line with the metric, the roofline of the dominant kernel
 (the fp32 MFMA implicit-GEMM ResBlock convolutions, timed with HIP events on
 the session stream over the timed steps) and a CPU baseline (the numpy
 oracle on a bounded 1 s sample of the same workload, on this host).
+
+``--workload hubert`` measures BASELINE config 3 instead (HuBERT-base
+encoder, 10 s of 16 kHz audio -> [1, 499, 768]) and ``--workload dec48k-b8``
+config 4 (48k GeneratorNSF, 8 chunks of 6 s as one batch); each prints its
+own JSON line in the same format.  The default run is config 2.
 """
 
 from __future__ import annotations
@@ -85,8 +90,162 @@ def calibrate_copy(mib: int):
     return 0
 
 
+def bench_hubert(args):
+    """HuBERT-base, 160 000 samples at 16 kHz, batch 1."""
+    from rvc_hip import _hip, synthetic as syn
+    from rvc_hip.hip_ops import get_context
+    from rvc_hip.hubert import HipHubert
+
+    T = 160000
+    sd = syn.make_hubert_weights(syn.HUBERT_BASE, seed=0)
+    ctx = get_context()
+    hub = HipHubert(sd, ctx=ctx)
+    _log(f"bench: device {_hip.device_name()}; HuBERT weights resident")
+    x = syn.make_hubert_input(T, seed=3)
+    L = hub.frames(T)
+    xid = ctx.upload(x)
+    oid = ctx.alloc(L * 768)
+
+    def step():
+        hub.encode_dev(xid, 1, T, oid, version=2)
+
+    for _ in range(args.warmup):
+        step()
+    hub.set_timing("hub.ffn")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = time.perf_counter() - t0
+    fam = hub.get_timing()
+    hub.set_timing("")
+    breakdown = {}
+    for tag in () if args.quick else ("hub.conv0", "hub.gn", "hub.conv", "hub.proj", "hub.pos", "hub.qkv", "hub.attn",
+                                      "hub.o", "hub.ln", "hub.ffn"):
+        hub.set_timing(tag)
+        step()
+        t = hub.get_timing()
+        breakdown[tag] = {"ms": round(t["ms"], 4),
+                          "tflops": round(t["flops"] / (t["ms"] / 1e3) / 1e12, 2) if t["ms"] > 0 else None,
+                          "gbs": round(t["bytes"] / (t["ms"] / 1e3) / 1e9, 1) if t["ms"] > 0 else None}
+    hub.set_timing("")
+    audio_s = T / 16000.0
+    value = audio_s * args.steps / dt
+    n = max(fam["launches"], 1)
+    avg_s = fam["ms"] / 1e3 / n
+    achieved = fam["flops"] / n / avg_s / 1e12 if avg_s > 0 else 0.0
+    roofline = {"kernel": "conv1d_mfma (HuBERT FFN 1x1 convs 768->3072->768)", "bound": "mfma",
+                "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n // args.steps,
+                "share_of_step": round(fam["ms"] / (dt * 1e3), 3)}
+    cpu = None
+    if not (args.no_cpu_baseline or args.quick):
+        from oracle import hubert_ref
+
+        ref = hubert_ref.HubertRef(sd)
+        xs = syn.make_hubert_input(16000, seed=7)
+        ref.encode(xs[:, :4000])
+        t0 = time.perf_counter()
+        ref.encode(xs)
+        cdt = time.perf_counter() - t0
+        cpu = {"value": 1.0 / cdt, "unit": "audio-s/s", "cores": _blas_threads(), "kind": "port",
+               "sample": f"1 s (16 000 samples) of the config-3 encode (same weights), numpy oracle, 1 run after "
+                         f"a warm-up, {cdt:.2f} s wall"}
+    line = {
+        "metric": "audio-sec encoded/sec (HuBERT-base, 10 s @16 kHz, 1 GPU)", "value": round(value, 2),
+        "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded input, random-init weights)",
+        "config": {"workload": "config 3: HuBERT-base encoder, 160000 samples @16 kHz -> [1,499,768], batch 1, fp32",
+                   "samples": T, "frames": L, "batch": 1},
+        "roofline": roofline, "cpu_baseline": cpu, "breakdown": breakdown,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_dec48(args):
+    """48k GeneratorNSF, 8 chunks of 6 s (P=600) as one batch."""
+    from rvc_hip import _hip, synthetic as syn
+    from rvc_hip.hip_ops import get_context
+    from rvc_hip.synth import HipSynthesizer
+
+    geom = syn.GEOM_48K
+    w = syn.make_weights(geom, seed=0)
+    ctx = get_context()
+    s = HipSynthesizer(w, sr=geom.sr, ctx=ctx)
+    _log(f"bench: device {_hip.device_name()}; 48k weights resident")
+    B, P = 8, 600
+    ins = [syn.make_dec_inputs(geom, P, seed=60 + i) for i in range(B)]
+    z = np.concatenate([i["z"] for i in ins]).astype(np.float32)
+    f0 = np.concatenate([i["f0"] for i in ins]).astype(np.float32)
+    g = np.repeat(ins[0]["g"].reshape(1, -1), B, axis=0).astype(np.float32)
+    ns = np.concatenate([i["ns"].reshape(1, -1) for i in ins]).astype(np.float32)
+    ids = [ctx.upload(np.ascontiguousarray(a)) for a in (z, f0, g, ns)]
+    wave = ctx.alloc(B * P * geom.upp)
+
+    def step():
+        s.decode_dev(ids[0], ids[1], ids[2], ids[3], B, P, wave)
+
+    for _ in range(args.warmup):
+        step()
+    s.set_timing("dec.rb")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = time.perf_counter() - t0
+    rb = s.get_timing()
+    s.set_timing("")
+    audio_s = B * P / 100.0
+    value = audio_s * args.steps / dt
+    n = max(rb["launches"], 1)
+    avg_s = rb["ms"] / 1e3 / n
+    achieved = rb["flops"] / n / avg_s / 1e12 if avg_s > 0 else 0.0
+    roofline = {"kernel": "conv1d_mfma (GeneratorNSF ResBlock convs, all stages)", "bound": "mfma",
+                "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n // args.steps,
+                "share_of_step": round(rb["ms"] / (dt * 1e3), 3)}
+    cpu = None
+    if not (args.no_cpu_baseline or args.quick):
+        from oracle import vits_ref
+
+        dec = vits_ref.GeneratorNSF(w, vits_ref.VitsConfig(w, sr=geom.sr))
+        d = syn.make_dec_inputs(geom, 100, seed=9)
+        dec.forward(d["z"][:, :, :10], d["f0"][:, :10], d["g"], d["ns"][:, :10 * geom.upp])
+        t0 = time.perf_counter()
+        dec.forward(d["z"], d["f0"], d["g"], d["ns"])
+        cdt = time.perf_counter() - t0
+        cpu = {"value": 1.0 / cdt, "unit": "audio-s/s", "cores": _blas_threads(), "kind": "port",
+               "sample": f"1 s (P=100) of one config-4 chunk (same 48k weights), numpy oracle, 1 run after a "
+                         f"warm-up, {cdt:.2f} s wall"}
+    line = {
+        "metric": "audio-sec synthesized/sec (48k GeneratorNSF, 8 x 6 s chunks as batch 8, 1 GPU)",
+        "value": round(value, 2), "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded inputs, random-init weights)",
+        "config": {"workload": "config 4: RVC v2 48k GeneratorNSF, 8 chunks x P=600 (6 s) as batch 8, fp32",
+                   "frames": P, "batch": B, "sample_rate": geom.sr, "chunk_audio_s_per_step": audio_s},
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+
+        return int(max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"),
+                       default=1))
+    except Exception:  # noqa: BLE001
+        return 1
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", default="synth40k", choices=("synth40k", "hubert", "dec48k-b8"),
+                    help="synth40k: BASELINE config 2 (default); hubert: config 3; dec48k-b8: config 4")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -104,6 +263,10 @@ def main():
         print(f"bench.py measures one MI355X only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "hubert":
+        return bench_hubert(args)
+    if args.workload == "dec48k-b8":
+        return bench_dec48(args)
 
     from rvc_hip import _hip, synthetic as syn
     from rvc_hip.hip_ops import get_context

@@ -49,7 +49,10 @@ __device__ __forceinline__ float apply_act(float v, int act, float slope) {
 
 // S: input stride (output i reads inputs from i*S), a template parameter so
 // the staged window and the B-operand addressing fold it at compile time.
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1>
+// KMAX: most taps of any group of the launch; it sizes the register
+// prefetch of the weights (1 for the plain GEMMs of 1x1 convolutions, which
+// then afford wide channel chunks).
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1, int KMAX = kConvTapsMax>
 struct Cfg {
   static constexpr int NWM = BM / WM;
   static constexpr int NWN = BN / WN;
@@ -58,10 +61,10 @@ struct Cfg {
   static constexpr int TM = WM / 32;
   static constexpr int TN = WN / 32;
   static constexpr int BKT = BK * SK;
-  static constexpr int XWMAX = BN * S + kConvHaloMax;
+  static constexpr int XWMAX = BN * S + (KMAX > 1 ? kConvHaloMax : 0);
   static constexpr int XPT = (BKT * XWMAX + NT - 1) / NT;
   static constexpr int W4ROW = BM / 4;
-  static constexpr int WPT = (kConvTapsMax * BKT * W4ROW + NT - 1) / NT;
+  static constexpr int WPT = (KMAX * BKT * W4ROW + NT - 1) / NT;
   static size_t lds_bytes(int K, int dil) {
     const int XW = BN * S + (K > 0 ? (K - 1) * dil : 0);
     const size_t stage = sizeof(float) * ((size_t)BKT * XW + (size_t)K * BKT * BM);
@@ -70,17 +73,22 @@ struct Cfg {
   }
 };
 
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_kernel(ConvLaunch a) {
-  using C = Cfg<BM, BN, WM, WN, BK, SK, S>;
+  using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX>;
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = C::BKT;
   constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
   static_assert(BK % 2 == 0 && BKT % 4 == 0, "channel chunk must be a multiple of 4");
 
   const int b = blockIdx.z % a.B;
-  const int gi = blockIdx.z / a.B;
+  const int gi = (blockIdx.z / a.B) % a.n_groups;
+  const int ks = blockIdx.z / (a.B * a.n_groups);  // channel split of a split-K launch
   const ConvGroup& G = a.g[gi];
   const int i0 = blockIdx.x * BN;
+  // input channels of this workgroup: all, or one split of a.ksplit
+  const int csplit = a.ksplit > 1 ? a.csplit : a.C_in;
+  const int ci_lo = ks * csplit;
+  const int ci_hi = min(a.C_in, ci_lo + csplit);
   if (i0 >= G.n_out) return;  // uniform for the whole workgroup, before any barrier
   const int co0 = blockIdx.y * BM;
   const int K = G.K;
@@ -125,7 +133,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
       const int ci = ci0 + r;
       const int t = tbase + j;
       float v = 0.f;
-      if (idx < nx && ci < a.C_in && t >= 0 && t < a.L_in) v = xb[(long long)ci * a.xc + t];
+      if (idx < nx && ci < ci_hi && t >= 0 && t < a.L_in) v = xb[(long long)ci * a.xc + t];
       xr[e] = v;
     }
 #pragma unroll
@@ -136,7 +144,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
       const int k = row / BKT;
       const int ci = ci0 + (row - k * BKT);
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (idx < nw4 && ci < a.C_in && co0 + 4 * c4 < a.w_ld)
+      if (idx < nw4 && ci < ci_hi && co0 + 4 * c4 < a.w_ld)
         v = *reinterpret_cast<const float4*>(G.w + ((long long)k * a.C_in + ci) * a.w_ld + co0 + 4 * c4);
       wreg[e] = v;
     }
@@ -158,13 +166,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
     }
   };
 
-  if (K > 0) {
-    const int nchunk = (a.C_in + BKT - 1) / BKT;
-    gload(0);
+  if (K > 0 && ci_hi > ci_lo) {
+    const int nchunk = (ci_hi - ci_lo + BKT - 1) / BKT;
+    gload(ci_lo);
     for (int c = 0; c < nchunk; ++c) {
       lstore();
       __syncthreads();
-      if (c + 1 < nchunk) gload((c + 1) * BKT);
+      if (c + 1 < nchunk) gload(ci_lo + (c + 1) * BKT);
       for (int k = 0; k < K; ++k) {
         const float* wk_ = ws + (k * BKT + wk * BK) * BM + wm * WM + l32;
         const float* xk = xs + wk * BK * XW + (wn * WN + l32) * S + k * dil;
@@ -214,6 +222,25 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
     }
   }
 
+  if (a.ksplit > 1) {
+    // split-K partial sums: part[ks][b][co][i]; splitk_reduce_kernel adds the
+    // splits in order and applies the epilogue
+    float* pp = a.part + (((long long)ks * a.B + b) * a.C_out) * G.n_out;
+#pragma unroll
+    for (int m = 0; m < TM; ++m)
+#pragma unroll
+      for (int n = 0; n < TN; ++n) {
+        const int i = i0 + wn * WN + n * 32 + l32;
+        if (i >= G.n_out) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int co = co0 + wm * WM + m * 32 + (r & 3) + 4 * half + 8 * (r >> 2);
+          if (co < a.C_out) pp[(long long)co * G.n_out + i] = acc[m][n][r];
+        }
+      }
+    return;
+  }
+
   // ---- fused epilogue ----
   const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
   float* ob = G.out + (long long)b * a.ob;
@@ -247,6 +274,32 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
   }
 }
 
+// out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
+// added in index order (deterministic), one thread per output element.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(ConvLaunch a) {
+  const ConvGroup& G = a.g[0];
+  const long long n = (long long)a.B * a.C_out * G.n_out;
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int i = (int)(e % G.n_out);
+  const int co = (int)((e / G.n_out) % a.C_out);
+  const int b = (int)(e / ((long long)G.n_out * a.C_out));
+  float v = a.part[e];
+  for (int s = 1; s < a.ksplit; ++s) v = v + a.part[e + (long long)s * n];
+  if (G.bias) v = v + G.bias[co];
+  if (a.bias2) v = v + a.bias2[(long long)b * a.bias2b + co];
+  const long long t = (long long)i * G.out_step + G.out_off;
+  if (G.res) v = v + G.res[(long long)b * a.rb + (long long)co * a.rc + t];
+  v = apply_act(v, a.out_act, a.out_slope);
+  float* o = G.out + (long long)b * a.ob + (long long)co * a.oc + t;
+  if (G.combine == COMB_ADD) {
+    v = *o + v;
+  } else if (G.combine == COMB_ADD_DIV) {
+    v = (*o + v) / a.div;
+  }
+  *o = v;
+}
+
 constexpr size_t kLdsLimit = 65536;
 
 int max_n_out(const ConvLaunch& a) {
@@ -255,16 +308,59 @@ int max_n_out(const ConvLaunch& a) {
   return n;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1, int KMAX = kConvTapsMax>
 bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
-  using C = Cfg<BM, BN, WM, WN, BK, SK, S>;
+  using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX>;
   size_t lds = 0;
   for (int g = 0; g < a.n_groups; ++g) lds = std::max(lds, C::lds_bytes(a.g[g].K, a.g[g].dil));
   if (lds > kLdsLimit) return false;
-  dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B);
-  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S>), grid, dim3(C::NT), lds, s, a);
+  dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B * std::max(a.ksplit, 1));
+  for (int g = 0; g < a.n_groups; ++g) RVC_CHECK(a.g[g].K <= KMAX, "conv1d_mfma: taps exceed the configuration");
+  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX>), grid, dim3(C::NT), lds, s, a);
   check_launch("conv1d_mfma");
+  if (a.ksplit > 1) {
+    const long long n = (long long)a.B * a.C_out * a.g[0].n_out;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+    check_launch("splitk_reduce");
+  }
   return true;
+}
+
+// Split-K plan for a single-group stride-1 launch whose output tiles alone
+// cannot fill the GPU: 128 x 128 (or 64 x 128) tiles and the input channels
+// cut into S splits of whole BKT-channel chunks (at least two chunks each),
+// so tiles x S reaches about 640 workgroups.  Depends on the per-item tile
+// count only, never on B, so batched calls keep the per-chunk results.
+long long n_blocks(const ConvLaunch& a, int BM, int BN);
+
+struct SplitPlan {
+  int S = 1, csplit = 0, BM = 0;
+};
+SplitPlan split_plan(const ConvLaunch& a) {
+  SplitPlan p;
+  if (a.n_groups != 1 || (a.g[0].in_step > 1) || a.g[0].K < 1) return p;
+  const bool gemm = a.g[0].K == 1;
+  int BM = 0, BKT = 0;
+  if (a.C_out % 128 == 0) {
+    BM = 128;
+    BKT = gemm ? 32 : 8;
+  } else if (a.C_out % 64 == 0) {
+    BM = 64;
+    BKT = gemm ? 32 : 16;
+  } else {
+    return p;
+  }
+  if (n_blocks(a, 64, 128) >= 384) return p;  // the tile grid alone fills the GPU
+  const long long nb = n_blocks(a, BM, 128);
+  const int max_s = a.C_in / (2 * BKT);
+  int S = (int)std::min<long long>((640 + nb - 1) / nb, max_s);
+  if (S < 2) return p;
+  const int chunks = (a.C_in + BKT - 1) / BKT;
+  const int per = (chunks + S - 1) / S;
+  p.csplit = per * BKT;
+  p.S = (a.C_in + p.csplit - 1) / p.csplit;
+  p.BM = BM;
+  return p;
 }
 
 // Workgroups per batch item.  The tile choice deliberately ignores B: the
@@ -277,6 +373,11 @@ long long n_blocks(const ConvLaunch& a, int BM, int BN) {
 }
 
 }  // namespace
+
+size_t conv1d_mfma_split_floats(const ConvLaunch& a) {
+  const SplitPlan p = split_plan(a);
+  return p.S > 1 ? (size_t)p.S * a.B * a.C_out * a.g[0].n_out : 0;
+}
 
 bool conv1d_mfma_supported(int K, int dil) {
   return K >= 0 && K <= kConvTapsMax && dil >= 1 && (K > 0 ? (K - 1) * dil : 0) <= kConvHaloMax;
@@ -311,6 +412,26 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
     if (!ok) ok = launch_cfg<32, 64, 32, 32, 8, 4, 2>(a, s) || launch_cfg<32, 64, 32, 32, 4, 4, 2>(a, s);
     RVC_CHECK(ok, "conv1d_mfma: no tile configuration fits the LDS budget");
     return;
+  }
+  if (a.part && a.part_floats > 0) {
+    const SplitPlan p = split_plan(a);
+    if (p.S > 1 && (size_t)p.S * a.B * a.C_out * a.g[0].n_out <= a.part_floats) {
+      ConvLaunch sa = a;
+      sa.ksplit = p.S;
+      sa.csplit = p.csplit;
+      if (a.g[0].K == 1)
+        ok = p.BM == 128 ? launch_cfg<128, 128, 64, 64, 32, 1, 1, 1>(sa, s) : launch_cfg<64, 128, 32, 64, 32, 1, 1, 1>(sa, s);
+      else
+        ok = p.BM == 128 ? launch_cfg<128, 128, 64, 64, 8, 1>(sa, s) : launch_cfg<64, 128, 32, 64, 16, 1>(sa, s);
+      if (ok) return;
+    }
+  }
+  int kmax = 0;
+  for (int g = 0; g < a.n_groups; ++g) kmax = std::max(kmax, a.g[g].K);
+  if (kmax == 1) {  // 1x1 convolutions: plain GEMMs with 32-channel chunks
+    if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= want) ok = launch_cfg<128, 128, 64, 64, 32, 1, 1, 1>(a, s);
+    if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want) ok = launch_cfg<64, 128, 32, 64, 32, 1, 1, 1>(a, s);
+    if (ok) return;
   }
   if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)

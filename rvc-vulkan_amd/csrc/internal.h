@@ -103,11 +103,18 @@ struct ConvLaunch {
   int in_act;  float in_slope;
   int out_act; float out_slope;
   float div;
+  // split-K over workgroups (single-group stride-1 launches): scratch for the
+  // partial sums, filled in by the launcher when part_floats suffices
+  float* part;
+  size_t part_floats;
+  int ksplit, csplit;  // set by the launcher
 };
 
 // MFMA implicit-GEMM conv1d (input stride 1 or 2, the same for every group
 // of a launch), K <= kConvTapsMax and (K-1)*dil <= kConvHaloMax.
 bool conv1d_mfma_supported(int K, int dil);
+// Scratch floats a launch needs for split-K partial sums (0: no split).
+size_t conv1d_mfma_split_floats(const ConvLaunch& a);
 void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s);
 
 // packed-weight leading dimension for C_out output channels

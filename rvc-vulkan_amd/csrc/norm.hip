@@ -56,6 +56,46 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const float* x, con
   for (int c = threadIdx.x; c < cols; c += blockDim.x) orow[c] = (xr[c] - mean) / den * g[c] + b[c];
 }
 
+// Channel-major LayerNorm with one wavefront per column (b, t): the C values
+// sit in registers (NR per lane, C <= 64 * NR), the two reductions are wave
+// shuffles, so each column costs one read and one write pass and the grid
+// has B * L / 4 workgroups (enough to spread a 499-frame layer over the CUs).
+// Same formulas as layernorm_cols_kernel.
+template <int NR>
+__global__ __launch_bounds__(256) void layernorm_cols_wave_kernel(const float* x, const float* g, const float* b,
+                                                                  float* out, int C, int L, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= L) return;  // whole wave; no workgroup barrier below
+  const long long base = (long long)blockIdx.y * C * L + t;
+  float v[NR];
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = c < C ? x[base + (long long)c * L] : 0.f;
+    s += v[i];
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  const float mean = (float)(s / C);
+  double q = 0.0;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int c = lane + 64 * i;
+    if (c < C) {
+      const float d = v[i] - mean;
+      q += (double)d * d;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+  const float den = sqrtf((float)(q / C) + eps);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int c = lane + 64 * i;
+    if (c < C) out[base + (long long)c * L] = (v[i] - mean) / den * g[c] + b[c];
+  }
+}
+
 // GroupNorm with one channel per group on [B][C][L] (the normalisation runs
 // over L for each (b, c)), two-pass in float64 like the row LayerNorm, then
 // the per-channel affine and an activation:
@@ -169,8 +209,18 @@ void launch_layernorm_rows(const float* x, const float* g, const float* b, float
 void launch_layernorm_cols(const float* x, const float* g, const float* b, float* out, int B, int C, int L,
                            float eps, hipStream_t s) {
   if ((long long)B * L <= 0 || C <= 0) return;
-  dim3 grid((L + LN_COLS - 1) / LN_COLS, B);
-  hipLaunchKernelGGL(layernorm_cols_kernel, grid, dim3(LN_COLS * LN_GRP), 0, s, x, g, b, out, C, L, eps);
+  if (C <= 1024) {
+    dim3 grid((L + 3) / 4, B);
+    if (C <= 256)
+      hipLaunchKernelGGL(layernorm_cols_wave_kernel<4>, grid, dim3(256), 0, s, x, g, b, out, C, L, eps);
+    else if (C <= 512)
+      hipLaunchKernelGGL(layernorm_cols_wave_kernel<8>, grid, dim3(256), 0, s, x, g, b, out, C, L, eps);
+    else
+      hipLaunchKernelGGL(layernorm_cols_wave_kernel<16>, grid, dim3(256), 0, s, x, g, b, out, C, L, eps);
+  } else {
+    dim3 grid((L + LN_COLS - 1) / LN_COLS, B);
+    hipLaunchKernelGGL(layernorm_cols_kernel, grid, dim3(LN_COLS * LN_GRP), 0, s, x, g, b, out, C, L, eps);
+  }
   check_launch("layernorm_cols");
 }
 

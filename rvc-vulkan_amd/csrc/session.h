@@ -202,7 +202,15 @@ struct SessionBase {
       if (g.res) bytes += 4.0 * outs;
       if (g.combine != COMB_STORE) bytes += 4.0 * outs;
     }
-    run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
+    const size_t need = conv1d_mfma_split_floats(a);
+    if (need == 0) {
+      run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
+      return;
+    }
+    ConvLaunch sa = a;
+    sa.part = buf("splitk", need);
+    sa.part_floats = need;
+    run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(sa, eng->stream); });
   }
 };
 
