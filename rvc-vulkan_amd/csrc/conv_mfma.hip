@@ -21,9 +21,12 @@
 // and the 16 accumulator registers r of lane l hold
 //   row = (r%4) + 4*(l/32) + 8*(r/4), col = l%32.
 //
-// The fused epilogue adds bias (and an optional second per-channel term),
-// an optional residual, applies leaky-ReLU / ReLU / tanh / GELU and combines into
-// the output (store, accumulate, or accumulate-then-divide).  Output position
+// The fused epilogue: bias (and an optional second per-channel term), an
+// optional residual and, for an accumulating launch without activation, the
+// current output are the accumulators' starting values (loaded while the
+// first chunk stages); at the end leaky-ReLU / ReLU / tanh / GELU is applied
+// and the result combined into the output (store, accumulate, or
+// accumulate-then-divide).  Output position
 // i is written at i*out_step + out_off, which lets one phase of a polyphase
 // ConvTranspose1d use the same kernel.  A launch may carry up to
 // kMaxConvGroups independent convolutions with the same channel counts
@@ -73,8 +76,14 @@ struct Cfg {
   }
 };
 
+// At least two resident waves per SIMD (the 1x1 GEMM tiles fit three unaided):
+// without the cap the compiler spends registers on the accumulator-start
+// loads and drops the 128 x 128 tile to one wave per SIMD (measured 30 %
+// slower).
 template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_kernel(ConvLaunch a) {
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64)
+__attribute__((amdgpu_waves_per_eu(KMAX == 1 ? 1 : 2)))
+void conv1d_mfma_kernel(ConvLaunch a) {
   using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX>;
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = C::BKT;
   constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
@@ -117,6 +126,37 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
     for (int n = 0; n < TN; ++n)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.f;
+
+  // The accumulation starts from bias (+ the second per-channel term)
+  // (+ the residual) (+ the current output of an accumulating launch without
+  // activation).  These loads are issued with the first chunk's, so their
+  // latency hides behind its staging instead of stalling the epilogue.
+  // Split-K partials stay raw; with intra-workgroup split-K only the waves
+  // that run the epilogue (wk == 0) start from them.
+  const bool fold_out = G.combine == COMB_ADD && a.out_act == ACT_NONE;
+  const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
+  float* ob = G.out + (long long)b * a.ob;
+  const float* rb = G.res ? G.res + (long long)b * a.rb : nullptr;
+  if (a.ksplit <= 1 && wk == 0) {
+#pragma unroll
+    for (int m = 0; m < TM; ++m)
+#pragma unroll
+      for (int n = 0; n < TN; ++n) {
+        const int i = i0 + wn * WN + n * 32 + l32;
+        if (i >= G.n_out) continue;
+        const long long t = (long long)i * G.out_step + G.out_off;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int co = co0 + wm * WM + m * 32 + (r & 3) + 4 * half + 8 * (r >> 2);
+          if (co >= a.C_out) continue;
+          float v = G.bias ? G.bias[co] : 0.f;
+          if (bias2) v = v + bias2[co];
+          if (rb) v = v + rb[co * a.rc + t];
+          if (fold_out) v = v + ob[co * a.oc + t];
+          acc[m][n][r] = v;
+        }
+      }
+  }
 
   float xr[XPT];
   float4 wreg[WPT];
@@ -241,10 +281,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
     return;
   }
 
-  // ---- fused epilogue ----
-  const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
-  float* ob = G.out + (long long)b * a.ob;
-  const float* rb = G.res ? G.res + (long long)b * a.rb : nullptr;
+  // ---- fused epilogue (bias / residual / accumulate target already in acc) ----
 #pragma unroll
   for (int m = 0; m < TM; ++m) {
 #pragma unroll
@@ -257,13 +294,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64) void conv1d_mfma_k
         const int row = (r & 3) + 4 * half + 8 * (r >> 2);
         const int co = co0 + wm * WM + m * 32 + row;
         if (co >= a.C_out) continue;
-        float v = acc[m][n][r];
-        if (G.bias) v = v + G.bias[co];
-        if (bias2) v = v + bias2[co];
-        if (rb) v = v + rb[co * a.rc + t];
-        v = apply_act(v, a.out_act, a.out_slope);
+        float v = apply_act(acc[m][n][r], a.out_act, a.out_slope);
         float* o = ob + co * a.oc + t;
-        if (G.combine == COMB_ADD) {
+        if (G.combine == COMB_ADD && !fold_out) {
           v = *o + v;
         } else if (G.combine == COMB_ADD_DIV) {
           v = (*o + v) / a.div;
