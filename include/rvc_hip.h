@@ -58,6 +58,14 @@ int32_t rvc_mem_download(int64_t h, int64_t buf, float* dst, int64_t n);
 int32_t rvc_mem_download_bytes(int64_t h, int64_t buf, void* dst, int64_t nbytes);
 /* replaces rvc_mem_free         (engine/src/ffi.zig:222) */
 int32_t rvc_mem_free(int64_t h, int64_t buf);
+/* replaces rvc_mem_upload_to_batch (engine/src/ffi.zig:107): n uploads into existing buffers,
+ * sizes[i] floats from datas[i] into ids[i]; every id and size is checked before any copy */
+int32_t rvc_mem_upload_to_batch(int64_t h, int64_t n, const int64_t* sizes, const float* const* datas,
+                                const int64_t* ids);
+/* replaces rvc_mem_download_batch (engine/src/ffi.zig:199): count downloads, sizes[i] floats of
+ * buffer bufs[i] into dsts[i]; one wait at the end */
+int32_t rvc_mem_download_batch(int64_t h, const int64_t* bufs, uint8_t* const* dsts, const int64_t* sizes,
+                               int64_t count);
 
 /* ---------------------------------------------------------------- single ops */
 /* replaces rvc_matmul  (engine/src/ffi.zig:233): c[M,N] = a[M,K] @ b[K,N], row-major */
@@ -93,19 +101,46 @@ int32_t rvc_layernorm(int64_t h, int64_t x, int64_t gamma, int64_t beta, int64_t
                       int64_t cols, double eps);
 /* replaces rvc_softmax (engine/src/ffi.zig:604): row softmax */
 int32_t rvc_softmax(int64_t h, int64_t x, int64_t out, int64_t rows, int64_t cols);
+/* replaces rvc_rmsnorm (engine/src/ffi.zig:616): out = x / sqrt(mean(x^2) + eps) * gamma per row */
+int32_t rvc_rmsnorm(int64_t h, int64_t x, int64_t gamma, int64_t out, int64_t rows, int64_t cols, double eps);
 
 /* ---------------------------------------------------------------- record / commit */
 /* replaces rvc_batch_begin / add / commit / commit_async / wait / discard
- * (engine/src/ffi.zig:880-1017).  Supported op codes and parameter layout are
- * the reference's (engine/src/ffi.zig:888-929): 1 matmul, 2 conv1d, 3 add_inplace,
+ * (engine/src/ffi.zig:880-1017).  Op codes and parameter layout are the
+ * reference's (engine/src/ffi.zig:888-929): 1 matmul, 2 conv1d, 3 add_inplace,
  * 4 mul_inplace, 5 conv_t1d, 6 leaky_relu, 7 copy, 8 softmax, 9 layer_norm,
- * 14 relu, 18 gating, 19 transpose. */
+ * 10 gelu, 11 bias_add, 12 attn_qk, 13 attn_sv, 14 relu, 15 group_norm,
+ * 16 banded_attn_qk, 17 banded_attn_sv, 18 gating, 19 transpose.  Codes 20-42
+ * (training backward ops, 2-D conv, im2col, AdamW scalars) are rejected.
+ * Every record is checked when it is added (buffers, sizes, parameters). */
 int32_t rvc_batch_begin(int64_t h);
 int32_t rvc_batch_add(int64_t h, int32_t op, int64_t a, int64_t b, int64_t c, int64_t p0, int64_t p1,
                       int64_t p2, int64_t p3, int64_t p4, int64_t p5, int64_t p6, int64_t p7, int64_t p8,
                       int64_t p9, int64_t p10);
 /* replaces rvc_batch_add_copy_seg (engine/src/ffi.zig:753): dst[a_off..+n) = src[b_off..+n) */
 int32_t rvc_batch_add_copy_seg(int64_t h, int64_t a, int64_t b, int64_t n, int64_t a_off, int64_t b_off);
+/* replaces rvc_batch_add_add_seg / mul_seg (engine/src/ffi.zig:779, :805): a[a_off..+n) (+|*)= b[b_off..+n) */
+int32_t rvc_batch_add_add_seg(int64_t h, int64_t a, int64_t b, int64_t n, int64_t a_off, int64_t b_off);
+int32_t rvc_batch_add_mul_seg(int64_t h, int64_t a, int64_t b, int64_t n, int64_t a_off, int64_t b_off);
+/* replaces rvc_batch_add_leaky_seg (engine/src/ffi.zig:832): a[a_off..+n) = leaky(a), slope as f32 bits */
+int32_t rvc_batch_add_leaky_seg(int64_t h, int64_t a, int64_t n, int64_t a_off, int64_t slope);
+/* replaces rvc_batch_add_gelu_seg (engine/src/ffi.zig:858): a[a_off..+n) = gelu(a) (erf form) */
+int32_t rvc_batch_add_gelu_seg(int64_t h, int64_t a, int64_t n, int64_t a_off);
+/* replaces rvc_batch_add_conv1d_seg (engine/src/ffi.zig:703): a=x b=w c=bias(0=none), p0..p8 as
+ * op 2 (pad_r must equal pad_l), p9=out; writes output columns [lo_off, lo_off+seg_len) of the
+ * full conv into rows of length l_out_full (lo_off + seg_len <= l_out_full) */
+int32_t rvc_batch_add_conv1d_seg(int64_t h, int64_t a, int64_t b, int64_t c, int64_t p0, int64_t p1,
+                                 int64_t p2, int64_t p3, int64_t p4, int64_t p5, int64_t p6, int64_t p7,
+                                 int64_t p8, int64_t p9, int64_t seg_len, int64_t lo_off, int64_t l_out_full);
+/* replaces rvc_batch_add_conv_t1d_seg (engine/src/ffi.zig:636): p0..p8 as op 5, p9=out; output
+ * columns [lo_off, lo_off+l_out) into rows of length l_out_full; only input columns
+ * [in_off, in_off+l_in_seg) (within the row of length L) contribute; vx/vw/vb/vo are byte offsets
+ * of sub-views into x/w/bias/out (-1 = none, else a multiple of 4) */
+int32_t rvc_batch_add_conv_t1d_seg(int64_t h, int64_t a, int64_t b, int64_t c, int64_t p0, int64_t p1,
+                                   int64_t p2, int64_t p3, int64_t p4, int64_t p5, int64_t p6, int64_t p7,
+                                   int64_t p8, int64_t p9, int64_t l_out, int64_t l_in_seg, int64_t in_off,
+                                   int64_t lo_off, int64_t l_out_full, int64_t vx, int64_t vw, int64_t vb,
+                                   int64_t vo);
 int32_t rvc_batch_commit(int64_t h);
 int32_t rvc_batch_commit_async(int64_t h);
 int32_t rvc_batch_wait(int64_t h);
@@ -116,6 +151,58 @@ int32_t rvc_batch_discard(int64_t h);
 int32_t rvc_device_name(char* buf, int64_t buf_size);
 /* replaces rvc_last_error (engine/src/ffi.zig:1110) */
 int32_t rvc_last_error(char* buf, int64_t buf_size);
+/* replaces rvc_ts_stats / rvc_ts_reset (engine/src/ffi.zig:1124, :1136): with RVC_TS=1 set when the
+ * engine is created, GPU-busy nanoseconds (HIP events around every submission) and the submission
+ * count since creation or the last reset; zeros otherwise */
+int32_t rvc_ts_stats(int64_t h, int64_t* busy_ns_out, int64_t* submits_out);
+int32_t rvc_ts_reset(int64_t h);
+/* replaces rvc_mem_stats (engine/src/ffi.zig:1147): every buffer is its own device allocation, so the
+ * suballocator / free-list / staging outputs are 0; buf_count, buf_bytes, max_buf_bytes are the live
+ * buffers', direct_bytes adds the engine's weight-packing scratch */
+int32_t rvc_mem_stats(int64_t h, int64_t* sub_total_out, int64_t* sub_chunks_out, int64_t* sub_free_bytes_out,
+                      int64_t* sub_free_blocks_out, int64_t* buf_count_out, int64_t* buf_bytes_out,
+                      int64_t* staging_up_out, int64_t* staging_dn_out, int64_t* direct_bytes_out,
+                      int64_t* max_buf_bytes_out, int64_t* max_buf_sub_out);
+/* replaces rvc_mem_top (engine/src/ffi.zig:1181): the n largest live buffers as (bytes, 0, device
+ * address) triples into out[3n]; returns the count written or -1 */
+int64_t rvc_mem_top(int64_t h, int64_t n, int64_t* out);
+/* replaces rvc_probe_extensions (engine/src/ffi.zig:1426): "shaderFloat16=1,VK_KHR_cooperative_matrix=1,
+ * VK_KHR_shader_float16_int8=1,arch=<gfx name>" (the capabilities those flags stand for, on the HIP
+ * device), NUL-terminated; -1 if buf_size is too small */
+int32_t rvc_probe_extensions(int64_t h, char* buf, int64_t buf_size);
+
+/* ---------------------------------------------------------------- not provided
+ * Exported so the reference's loader (runtime/_vulkan.py:148-278 binds every
+ * symbol) can load this library; each returns -1 with a message.  They serve
+ * the RMVPE pitch model and training, outside the synthesis path:
+ * rvc_matmul_f16 (ffi.zig:246), rvc_conv2d (:378), rvc_conv_t2d (:428),
+ * rvc_insert_zeros_2x (:483), rvc_batch_add_conv2d (:1196),
+ * rvc_batch_add_conv_t2d (:1246), rvc_batch_add_im2col_1d (:1304),
+ * rvc_batch_add_im2col_2d (:1341), rvc_batch_add_gru (:1377), rvc_gru (:1394),
+ * rvc_batch_add_gru_sync (:1411). */
+int32_t rvc_matmul_f16(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t ih,
+                   int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h, int64_t pad_w, int64_t stride_h,
+                   int64_t stride_w);
+int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, int64_t c_in, int64_t ih, int64_t iw,
+                     int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                     int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out);
+int32_t rvc_insert_zeros_2x(int64_t h, int64_t x, int64_t out, int64_t c, int64_t ih, int64_t iw);
+int32_t rvc_batch_add_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                             int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h,
+                             int64_t pad_w, int64_t stride_h, int64_t stride_w);
+int32_t rvc_batch_add_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                               int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t sh,
+                               int64_t sw, int64_t ph, int64_t pw, int64_t opad_h, int64_t opad_w, int64_t h_out,
+                               int64_t w_out);
+int32_t rvc_batch_add_im2col_1d(int64_t h, int64_t x, int64_t out, int64_t B, int64_t c, int64_t t, int64_t o_l,
+                                int64_t k_dil, int64_t stride, int64_t pad_l, int64_t dilation);
+int32_t rvc_batch_add_im2col_2d(int64_t h, int64_t x, int64_t out, int64_t B, int64_t c, int64_t ih, int64_t iw,
+                                int64_t oh, int64_t ow, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
+                                int64_t pw);
+int32_t rvc_batch_add_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
+int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
+int32_t rvc_batch_add_gru_sync(int64_t h, int64_t a, int64_t t, int64_t hdim);
 
 /* ---------------------------------------------------------------- synthesis session
  * No counterpart in the reference ABI.  A session owns device-resident,

@@ -74,19 +74,21 @@ __global__ __launch_bounds__(256) void conv_t1d_direct_kernel(ConvTArgs a) {
   const int co = (int)((idx / a.n_out) % a.C_out);
   const int b = (int)(idx / ((long long)a.n_out * a.C_out));
   const float* xb = a.x + (long long)b * a.xb;
+  const int lo = a.win_len > 0 ? max(a.win_lo, 0) : 0;
+  const int hi = a.win_len > 0 ? min(a.win_lo + a.win_len, a.L_in) : a.L_in;
   float acc = 0.f;
   for (int k = 0; k < a.K; ++k) {
-    const int num = o + a.padding - k * a.dil;
+    const int num = o + a.o_off + a.padding - k * a.dil;
     if (num < 0 || num % a.stride != 0) continue;
     const int t = num / a.stride;
-    if (t >= a.L_in) continue;
+    if (t < lo || t >= hi) continue;
     for (int ci = 0; ci < a.C_in; ++ci)
       acc += act_in(xb[(long long)ci * a.xc + t], a.in_act, a.in_slope) *
              a.w[((long long)ci * a.C_out + co) * a.K + k];
   }
   float v = acc;
   if (a.bias) v = v + a.bias[co];
-  float* out = a.out + (long long)b * a.ob + (long long)co * a.oc + o;
+  float* out = a.out + (long long)b * a.ob + (long long)co * a.oc + o + a.o_off;
   if (a.combine == COMB_ADD) v = *out + v;
   *out = v;
 }

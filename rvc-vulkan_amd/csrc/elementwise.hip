@@ -55,6 +55,14 @@ __global__ void fill_kernel(float* a, long long n, float v) {
 __global__ void add_gelu_kernel(float* o, const float* a, const float* p, long long n) {
   GRID_STRIDE(i, n) o[i] = a[i] + gelu_as(p[i]);
 }
+// in-place GELU (erf form, the A&S 7.1.26 erf of gelu_as)
+__global__ void gelu_kernel(float* a, long long n) {
+  GRID_STRIDE(i, n) a[i] = gelu_as(a[i]);
+}
+// out[i] = a[i] + bias[i % cols]  (row-major [rows][cols] plus a per-column bias)
+__global__ void bias_add_kernel(float* o, const float* a, const float* bias, long long n, long long cols) {
+  GRID_STRIDE(i, n) o[i] = a[i] + bias[i % cols];
+}
 __global__ void avg3_kernel(float* o, const float* a, const float* b, const float* c, long long n) {
   GRID_STRIDE(i, n) o[i] = ((a[i] + b[i]) + c[i]) / 3.0f;
 }
@@ -319,6 +327,16 @@ void launch_add_gelu(float* out, const float* a, const float* p, long long n, hi
   if (n <= 0) return;
   hipLaunchKernelGGL(add_gelu_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, p, n);
   check_launch("add_gelu");
+}
+void launch_gelu(float* a, long long n, hipStream_t s) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(gelu_kernel, dim3(capped_grid(n)), dim3(256), 0, s, a, n);
+  check_launch("gelu");
+}
+void launch_bias_add(float* out, const float* a, const float* bias, long long n, long long cols, hipStream_t s) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(bias_add_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, bias, n, cols);
+  check_launch("bias_add");
 }
 
 void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s) {

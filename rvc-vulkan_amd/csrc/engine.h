@@ -18,7 +18,7 @@ struct DevBuf {
 struct BatchOp {
   int op;
   long long a, b, c;
-  long long p[11];
+  long long p[20];  // p0..p10 of rvc_batch_add, or the longer parameter lists of the segment records
 };
 
 struct Engine {
@@ -34,6 +34,12 @@ struct Engine {
   // record/commit batch
   std::vector<BatchOp> batch;
   bool in_flight = false;
+  // GPU-busy accounting behind rvc_ts_stats, on when RVC_TS=1 at creation:
+  // every submission (a batch commit or a single-op call) is bracketed by
+  // two events, resolved when the stats are read.
+  bool ts_on = false;
+  long long ts_busy_ns = 0, ts_submits = 0;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> ts_pending;
 
   Engine();
   ~Engine();
@@ -43,6 +49,7 @@ struct Engine {
   float* fptr(long long id, long long n_floats, const char* what);  // validates size
   void* scratch_for(size_t bytes);
   void sync();
+  void ts_collect();  // sync, then fold the pending event pairs into ts_busy_ns
 };
 
 // Handle tables (handles are small sequential integers, never raw pointers,

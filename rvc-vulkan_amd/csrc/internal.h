@@ -147,6 +147,10 @@ struct ConvTArgs {
   int in_act; float in_slope;
   int combine;
   int B;
+  // Segment form: output index o is absolute column o + o_off of the full
+  // transposed conv (written there, row stride oc), and only input columns
+  // in [win_lo, win_lo + win_len) contribute (win_len == 0: the whole row).
+  int o_off, win_lo, win_len;
 };
 void launch_conv_t1d_direct(const ConvTArgs& a, hipStream_t s);
 
@@ -155,7 +159,10 @@ void launch_conv_t1d_direct(const ConvTArgs& a, hipStream_t s);
 // (launch_pack_convt_phase), ld packed_ld(C_out).  stride <= kMaxConvGroups.
 void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc, const float* const* w_phases,
                      const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
-                     int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine);
+                     int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine,
+                     int o_lo = 0, int x_shift = 0);
+// (Segment form: only output columns [o_lo, n_out) are computed, and x's
+// column 0 is input column x_shift of the full row, L its window length.)
 // taps of phase r of a stride-st ConvTranspose with K taps
 inline int convt_phase_taps(int K, int st, int r) { return r < K ? (K - r + st - 1) / st : 0; }
 
@@ -178,6 +185,10 @@ void launch_mul(float* c, const float* a, const float* b, long long n, hipStream
 void launch_fill(float* a, long long n, float v, hipStream_t s);
 // out = a + gelu(p)
 void launch_add_gelu(float* out, const float* a, const float* p, long long n, hipStream_t s);
+// a = gelu(a) in place (erf form, gelu_as)
+void launch_gelu(float* a, long long n, hipStream_t s);
+// out[i] = a[i] + bias[i % cols]
+void launch_bias_add(float* out, const float* a, const float* bias, long long n, long long cols, hipStream_t s);
 // out = ((a + b) + c) / 3   (the ResBlock average, runtime/models/vits.py:2225-2227)
 void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s);
 // out[i, :] = table[ids[i], :], ids int32 with negative wrap.
@@ -227,6 +238,12 @@ void launch_softmax_rows(const float* x, float* out, long long rows, int cols, h
 // One-channel-per-group GroupNorm over L of x[B][C][L], affine per channel, then act.
 void launch_groupnorm_rows_act(const float* x, const float* g, const float* b, float* out, int B, int C, long long L,
                                float eps, int act, hipStream_t s);
+// x [G][Cpg*S] standardised per row, affine of channel g*Cpg + i/S
+void launch_groupnorm_groups(const float* x, const float* g, const float* b, float* out, long long G, int Cpg,
+                             long long S, float eps, hipStream_t s);
+// out = x / sqrt(mean(x^2) + eps) * gamma, per row of [rows][cols]
+void launch_rmsnorm_rows(const float* x, const float* g, float* out, long long rows, int cols, float eps,
+                         hipStream_t s);
 
 // ---------------------------------------------------------------- attention
 // Windowed relative-position attention, all heads (emb_k = emb_v = null:
@@ -238,6 +255,15 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
                              float* scratch, int B, int H, int D, int P, int window, hipStream_t s);
 size_t relpos_attention_scratch_floats(int B, int H, int D, int P);
 size_t relpos_attention_max_frames();
+
+// Op-level attention on head-interleaved [T][C] q/k/v (head h in columns
+// [h*D, (h+1)*D)); used [2T-1][D] (relative table, m = s - t + T - 1) or null.
+//   scores [H][T][T] = q_h . (k_h + used[m])
+//   ctx [T][C]       = sum_s W[h][t][s] (v_h[s] + used[m])
+void launch_attn_scores(const float* q, const float* k, const float* used, float* out, int H, int T, int D, int C,
+                        hipStream_t s);
+void launch_attn_context(const float* w, const float* v, const float* used, float* out, int H, int T, int D, int C,
+                         hipStream_t s);
 
 // ---------------------------------------------------------------- matmul
 // c[M][N] = a[M][K] @ b[K][N], row-major (op-level rvc_matmul)

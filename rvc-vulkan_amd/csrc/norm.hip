@@ -127,6 +127,48 @@ __global__ __launch_bounds__(256) void groupnorm_rows_act_kernel(const float* x,
   }
 }
 
+// GroupNorm of the op-level ABI: x is [G][Cpg*S] (G groups, Cpg channels of
+// S elements each); every row is standardised over its Cpg*S values and
+// element i of row g gets the affine of channel g*Cpg + i/S
+// (engine/shaders/gn.comp:1-8).  Statistics two-pass in double.
+__global__ __launch_bounds__(256) void groupnorm_groups_kernel(const float* x, const float* g, const float* b,
+                                                               float* out, int Cpg, long long S, float eps) {
+  __shared__ double sh[256 / 64];
+  const long long row = blockIdx.x;
+  const long long n = (long long)Cpg * S;
+  const float* xr = x + row * n;
+  float* orow = out + row * n;
+  double s = 0.0;
+  for (long long i = threadIdx.x; i < n; i += blockDim.x) s += xr[i];
+  const float mean = (float)(block_sum_d(s, sh) / (double)n);
+  double v = 0.0;
+  for (long long i = threadIdx.x; i < n; i += blockDim.x) {
+    const float d = xr[i] - mean;
+    v += (double)d * d;
+  }
+  const float var = (float)(block_sum_d(v, sh) / (double)n);
+  const float den = sqrtf(var + eps);
+  const long long c0 = row * Cpg;
+  for (long long i = threadIdx.x; i < n; i += blockDim.x) {
+    const long long c = c0 + i / S;
+    orow[i] = (xr[i] - mean) / den * g[c] + b[c];
+  }
+}
+
+// RMSNorm over the last dim: out = x * (1 / sqrt(mean(x^2) + eps)) * gamma
+// (engine/shaders/rmsnorm.comp:1-6); the sum of squares accumulates in double.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const float* g, float* out, int cols,
+                                                           float eps) {
+  __shared__ double sh[256 / 64];
+  const long long row = blockIdx.x;
+  const float* xr = x + row * cols;
+  float* orow = out + row * cols;
+  double q = 0.0;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) q += (double)xr[i] * xr[i];
+  const float inv = 1.0f / sqrtf((float)(block_sum_d(q, sh) / (double)cols) + eps);
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) orow[i] = xr[i] * inv * g[i];
+}
+
 // Channel-major [B][C][L]: normalise over C for each (b, t).  A workgroup
 // owns LN_COLS consecutive columns; its LN_GRP thread groups split the
 // channels (coalesced reads along t) and combine partial sums in LDS.
@@ -230,6 +272,22 @@ void launch_groupnorm_rows_act(const float* x, const float* g, const float* b, f
   hipLaunchKernelGGL(groupnorm_rows_act_kernel, dim3((unsigned)((long long)B * C)), dim3(256), 0, s, x, g, b, out, C,
                      L, eps, act);
   check_launch("groupnorm_rows_act");
+}
+
+void launch_groupnorm_groups(const float* x, const float* g, const float* b, float* out, long long G, int Cpg,
+                             long long S, float eps, hipStream_t s) {
+  if (G <= 0 || Cpg <= 0 || S <= 0) return;
+  RVC_CHECK(G <= 0x7fffffffLL, "group_norm: too many groups");
+  hipLaunchKernelGGL(groupnorm_groups_kernel, dim3((unsigned)G), dim3(256), 0, s, x, g, b, out, Cpg, S, eps);
+  check_launch("groupnorm_groups");
+}
+
+void launch_rmsnorm_rows(const float* x, const float* g, float* out, long long rows, int cols, float eps,
+                         hipStream_t s) {
+  if (rows <= 0 || cols <= 0) return;
+  RVC_CHECK(rows <= 0x7fffffffLL, "rmsnorm: too many rows");
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, g, out, cols, eps);
+  check_launch("rmsnorm_rows");
 }
 
 void launch_softmax_rows(const float* x, float* out, long long rows, int cols, hipStream_t s) {

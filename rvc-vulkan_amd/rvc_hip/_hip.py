@@ -55,6 +55,8 @@ SYMBOLS = {
     "rvc_mem_download": (I32, [I64, I64, F32P, I64]),
     "rvc_mem_download_bytes": (I32, [I64, I64, VOIDP, I64]),
     "rvc_mem_free": (I32, [I64, I64]),
+    "rvc_mem_upload_to_batch": (I32, [I64, I64, I64P, ctypes.POINTER(F32P), I64P]),
+    "rvc_mem_download_batch": (I32, [I64, I64P, ctypes.POINTER(ctypes.POINTER(ctypes.c_uint8)), I64P, I64]),
     "rvc_matmul": (I32, [I64] * 7),
     "rvc_add": (I32, [I64] * 5),
     "rvc_mul": (I32, [I64] * 5),
@@ -68,15 +70,39 @@ SYMBOLS = {
     "rvc_copy": (I32, [I64] * 4),
     "rvc_layernorm": (I32, [I64] * 7 + [DBL]),
     "rvc_softmax": (I32, [I64] * 5),
+    "rvc_rmsnorm": (I32, [I64] * 6 + [DBL]),
     "rvc_batch_begin": (I32, [I64]),
     "rvc_batch_add": (I32, [I64, I32] + [I64] * 14),
     "rvc_batch_add_copy_seg": (I32, [I64] * 6),
+    "rvc_batch_add_add_seg": (I32, [I64] * 6),
+    "rvc_batch_add_mul_seg": (I32, [I64] * 6),
+    "rvc_batch_add_leaky_seg": (I32, [I64] * 5),
+    "rvc_batch_add_gelu_seg": (I32, [I64] * 4),
+    "rvc_batch_add_conv1d_seg": (I32, [I64] * 17),
+    "rvc_batch_add_conv_t1d_seg": (I32, [I64] * 23),
     "rvc_batch_commit": (I32, [I64]),
     "rvc_batch_commit_async": (I32, [I64]),
     "rvc_batch_wait": (I32, [I64]),
     "rvc_batch_discard": (I32, [I64]),
     "rvc_device_name": (I32, [CHARP, I64]),
     "rvc_last_error": (I32, [CHARP, I64]),
+    "rvc_ts_stats": (I32, [I64, I64P, I64P]),
+    "rvc_ts_reset": (I32, [I64]),
+    "rvc_mem_stats": (I32, [I64] + [I64P] * 11),
+    "rvc_mem_top": (I64, [I64, I64, I64P]),
+    "rvc_probe_extensions": (I32, [I64, CHARP, I64]),
+    # exported for the reference loader; each returns -1 with a message
+    "rvc_matmul_f16": (I32, [I64] * 7),
+    "rvc_conv2d": (I32, [I64] * 16),
+    "rvc_conv_t2d": (I32, [I64] * 19),
+    "rvc_insert_zeros_2x": (I32, [I64] * 6),
+    "rvc_batch_add_conv2d": (I32, [I64] * 16),
+    "rvc_batch_add_conv_t2d": (I32, [I64] * 20),
+    "rvc_batch_add_im2col_1d": (I32, [I64] * 11),
+    "rvc_batch_add_im2col_2d": (I32, [I64] * 15),
+    "rvc_batch_add_gru": (I32, [I64] * 7),
+    "rvc_gru": (I32, [I64] * 7),
+    "rvc_batch_add_gru_sync": (I32, [I64] * 4),
     "rvc_synth_create": (I64, [I64]),
     "rvc_synth_destroy": (I32, [I64]),
     "rvc_synth_set_weight": (I32, [I64, CHARP, F32P, I64P, I32]),

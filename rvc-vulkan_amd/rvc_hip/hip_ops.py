@@ -44,6 +44,7 @@ __all__ = [
     "mul_inplace",
     "layer_norm",
     "softmax",
+    "rmsnorm",
     "leaky_relu",
 ]
 
@@ -408,6 +409,32 @@ class HipContext:
 
         return self._run(go, t)
 
+    def rmsnorm(self, x, gamma, eps=1e-5, buf_gamma=None):
+        """out = x / sqrt(mean(x^2) + eps) * gamma over the last axis
+        (runtime/backend.py:309-317, runtime/vulkan_ops.py:1994-2019)."""
+        x = _as_f32(x, "rmsnorm x")
+        gamma = _as_f32(gamma, "rmsnorm gamma")
+        if gamma.ndim != 1:
+            raise ValueError(f"rmsnorm gamma must be 1-D, got {gamma.ndim}-D")
+        cols = gamma.shape[0]
+        if x.ndim < 1 or x.shape[-1] != cols:
+            raise ValueError(f"rmsnorm: x[-1]={x.shape[-1] if x.ndim else None} does not match gamma {gamma.shape}")
+        if x.size == 0:
+            return np.empty(x.shape, dtype=np.float32)
+        rows = x.size // cols
+        t = []
+
+        def go():
+            xi = self.upload(x)
+            t.append(xi)
+            gi = self._in(gamma, buf_gamma, t)
+            oi = self._out(x.size, t)
+            with self._lock:
+                _hip._check(self._lib.rvc_rmsnorm(self.handle, xi, gi, oi, rows, cols, float(eps)), "rvc_rmsnorm")
+            return self.download(oi, x.shape)
+
+        return self._run(go, t)
+
     def softmax(self, x):
         x = _as_f32(x, "softmax x")
         if x.ndim < 1:
@@ -489,6 +516,10 @@ def mul_inplace(a, b, buf_a=None, buf_b=None):
 
 def layer_norm(x, gamma, beta, eps=1e-5, buf_gamma=None, buf_beta=None):
     return get_context().layer_norm(x, gamma, beta, eps, buf_gamma=buf_gamma, buf_beta=buf_beta)
+
+
+def rmsnorm(x, gamma, eps=1e-5, buf_gamma=None):
+    return get_context().rmsnorm(x, gamma, eps, buf_gamma=buf_gamma)
 
 
 def softmax(x):

@@ -98,3 +98,48 @@ def test_synthetic_generator_is_seeded():
     assert syn.weights_digest(a) != syn.weights_digest(syn.make_weights(syn.GEOM_TINY, seed=4))
     f0 = syn.make_f0(200, np.random.default_rng(0))
     assert (f0 == 0).mean() >= 0.2 and f0.max() <= 400 and f0[f0 > 0].min() >= 80
+
+
+def test_reference_loader_symbols_bind(hip):
+    """Every symbol the reference's ctypes loader binds (runtime/_vulkan.py:
+    148-278, no try/except) is exported with the same argument count and
+    return width, so that loader can load librvc_hip.so via RVC_CORE_DLL."""
+    with open(os.path.join(GOLDEN, "reference_loader_symbols.json")) as f:
+        ref = json.load(f)["symbols"]
+    assert len(ref) == 56
+    lib = ctypes.CDLL(hip.so_path)
+    width = {"I32": ctypes.c_int32, "I64": ctypes.c_int64}
+    for name, spec in ref.items():
+        assert hasattr(lib, name), name
+        res, args = hip.SYMBOLS[name]
+        assert len(args) == spec["nargs"], (name, len(args), spec["nargs"])
+        assert res is width[spec["restype"]], name
+
+
+def test_not_provided_exports_fail_with_message(hip):
+    L = hip.get_lib()
+    assert L.rvc_conv2d(1, *([1] * 15)) == -1
+    assert "rvc_conv2d: not provided" in hip.last_error()
+    assert L.rvc_gru(1, 1, 1, 1, 1, 1, 1) == -1
+    assert "rvc_gru: not provided" in hip.last_error()
+    assert L.rvc_matmul_f16(1, 1, 1, 1, 1, 1, 1) == -1
+    assert L.rvc_batch_add_im2col_2d(1, *([1] * 14)) == -1
+
+
+def test_new_exports_reject_bad_handles(hip):
+    L = hip.get_lib()
+    a, b = ctypes.c_int64(), ctypes.c_int64()
+    assert L.rvc_ts_stats(424242, ctypes.byref(a), ctypes.byref(b)) == -1
+    assert hip.last_error() == "invalid engine handle"
+    assert L.rvc_ts_reset(424242) == -1
+    outs = [ctypes.c_int64() for _ in range(11)]
+    assert L.rvc_mem_stats(424242, *[ctypes.byref(o) for o in outs]) == -1
+    arr = (ctypes.c_int64 * 3)()
+    assert L.rvc_mem_top(424242, 1, arr) == -1
+    buf = ctypes.create_string_buffer(64)
+    assert L.rvc_probe_extensions(424242, buf, 64) == -1
+    assert L.rvc_rmsnorm(424242, 1, 2, 3, 1, 1, 1e-5) == -1
+    assert L.rvc_batch_add_gelu_seg(424242, 1, 1, 0) == -1
+    assert L.rvc_batch_add_conv_t1d_seg(424242, *([1] * 22)) == -1
+    assert L.rvc_batch_add(424242, 12, 1, 2, 3, *([1] * 11)) == -1
+    assert hip.last_error() == "invalid engine handle"

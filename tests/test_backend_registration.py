@@ -85,7 +85,7 @@ def test_op_registration_and_duplicate():
     # the op module exposes the dispatcher's op names (runtime/backend.py:205-316)
     mod = importlib.import_module(info["module"])
     for op in ("matmul", "add", "mul", "relu", "conv1d", "conv_transpose1d", "embedding", "add_inplace",
-               "mul_inplace", "layer_norm", "softmax"):
+               "mul_inplace", "layer_norm", "softmax", "rmsnorm"):
         assert callable(getattr(mod, op)), op
 
 
