@@ -38,11 +38,28 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 SR = 40000
 P_FRAMES = 1000           # 10 s at 100 frames/s
-CPU_SAMPLE_FRAMES = 100   # 1 s sample for the numpy baseline
+CPU_SAMPLE_FRAMES = 400   # 4 s sample for the numpy baseline (about 10 s of CPU work)
 
 
 def _log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "synth_40k_resblock_traffic.md")
+
+
+def profiled_traffic():
+    """HBM bytes per ResBlock launch from the committed PMC summary (FETCH_SIZE
+    and WRITE_SIZE runs of this benchmark, copy-calibrated; written by
+    ``python -m rvc_hip.profsum --traffic``), or None when it is absent."""
+    import re
+
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"resblock_traffic_bytes_per_launch: (\d+)", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(w, geom):
@@ -67,7 +84,7 @@ def cpu_baseline(w, geom):
     dt = time.perf_counter() - t0
     audio_s = CPU_SAMPLE_FRAMES / 100.0
     return {"value": audio_s / dt, "unit": "audio-s/s", "cores": int(threads), "kind": "port",
-            "sample": f"1 s (P={CPU_SAMPLE_FRAMES}) of the config-2 synthesis (same weights, 40k), "
+            "sample": f"{CPU_SAMPLE_FRAMES / 100:g} s (P={CPU_SAMPLE_FRAMES}) of the config-2 synthesis (same weights, 40k), "
                       f"numpy oracle, 1 run after a warm-up, {dt:.2f} s wall"}
 
 
@@ -320,7 +337,9 @@ def main():
     achieved = flops_launch / avg_s / 1e12 if avg_s > 0 else 0.0
     roofline = {"kernel": "conv1d_mfma (GeneratorNSF ResBlock convs, all stages)", "bound": "mfma",
                 "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": profiled_traffic(),
+                "algorithmic_bytes": int(rb["bytes"] / n_launch),
+                "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
                 "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n_launch // args.steps,
                 "share_of_step": round(rb["ms"] / (dt * 1e3), 3)}
 

@@ -18,7 +18,9 @@
    reaches through ``vulkan_ops.BatchRunner`` on the vulkan backend.
    ``bind_synthesizer`` builds a ``HipSynthesizer`` from a constructed
    reference ``SynthesizerTrn`` (its ``weight_dict`` and ``cfg``) so the caller
-   can route ``infer_controlled`` / ``dec.forward`` to it.
+   can route ``infer_controlled`` / ``dec.forward`` to it; ``bind_hubert``
+   does the same for a ``HubertEncoder`` (``runtime/models/hubert.py:355``),
+   routing ``encode`` / ``encode_batch`` to a ``HipHubert``.
 
 Every function takes the reference module or object as an argument, so this
 package never imports the reference and the same code registers against any
@@ -36,6 +38,7 @@ __all__ = [
     "make_session_backend",
     "register_session_backend",
     "bind_synthesizer",
+    "bind_hubert",
 ]
 
 BACKEND_NAME = "hip"
@@ -107,3 +110,16 @@ def bind_synthesizer(trn, ctx=None):
     from .synth import HipSynthesizer
 
     return HipSynthesizer(trn.weight_dict, geometry=trn.cfg, ctx=ctx)
+
+
+def bind_hubert(encoder, ctx=None):
+    """A ``HipHubert`` holding the weights of a constructed reference
+    ``HubertEncoder``: its float32 state dict ``encoder._sd`` (prefix-stripped
+    transformers keys, ``runtime/models/hubert.py:499-512``); the encoder's own
+    derived entries (keys starting with ``_``) are skipped, the weight norm of
+    the positional conv is applied again on the device side from
+    ``weight_g``/``weight_v`` or ``parametrizations.weight.original0/1``."""
+    from .hubert import HipHubert
+
+    sd = {k: v for k, v in encoder._sd.items() if not k.startswith("_")}
+    return HipHubert(sd, ctx=ctx)

@@ -85,6 +85,34 @@ class HipHubert:
                                                 out.ctypes.data_as(_F32P)), "rvc_hubert_encode")
         return out
 
+    def encode_batch(self, xs, version: int = 2) -> list:
+        """The reference's ``encode_batch`` (``runtime/models/hubert.py:593-656``):
+        a list of ``[1, T_i]`` (or ``[T_i]``) chunks of possibly different
+        lengths -> a list of ``[1, L_i, D]``, each equal to ``encode`` of that
+        chunk.  Chunks of equal length run as one batched call (bit-identical
+        to running them one by one), in input order."""
+        if version not in (1, 2):
+            raise ValueError(f"version must be 1 or 2, got {version}")
+        if isinstance(xs, np.ndarray):
+            xs = [xs]
+        xl = []
+        for x in xs:
+            x = np.asarray(x, dtype=np.float32)
+            if x.ndim == 1:
+                x = x[None, :]
+            if x.ndim != 2 or x.shape[0] != 1:
+                raise ValueError(f"each chunk must be [1, T], got {x.shape}")
+            xl.append(x)
+        out: list = [None] * len(xl)
+        by_len: dict = {}
+        for i, x in enumerate(xl):
+            by_len.setdefault(x.shape[1], []).append(i)
+        for idx in by_len.values():
+            y = self.encode(np.concatenate([xl[i] for i in idx], axis=0), version)
+            for j, i in enumerate(idx):
+                out[i] = y[j:j + 1]
+        return out
+
     def encode_dev(self, x_id: int, B: int, T: int, out_id: int, version: int = 2):
         _hip._check(self._lib.rvc_hubert_encode_dev(self.handle, int(x_id), int(B), int(T), int(version), int(out_id)),
                     "rvc_hubert_encode_dev")

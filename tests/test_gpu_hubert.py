@@ -101,3 +101,25 @@ def test_batch_equals_per_chunk(hub):
 def test_rejects_too_short_input(hub):
     with pytest.raises(ValueError):
         hub.encode(np.zeros((1, 300), np.float32))
+
+
+def test_encode_batch_ragged_and_bind(sd):
+    """encode_batch (runtime/models/hubert.py:593-656): ragged chunks -> each
+    equals encode of that chunk; bind_hubert reads a HubertEncoder-shaped
+    object's ``_sd`` (derived ``_`` entries skipped)."""
+    from rvc_hip import backend_hip
+
+    class Enc:  # the attribute bind_hubert reads from a reference HubertEncoder
+        pass
+
+    enc = Enc()
+    enc._sd = dict(sd)
+    enc._sd["_pos_conv_weight"] = np.zeros(3, np.float32)
+    hub = backend_hip.bind_hubert(enc)
+    xs = [syn.make_hubert_input(n, seed=s)[0] for n, s in ((6400, 1), (8000, 2), (6400, 3))]
+    got = hub.encode_batch(xs, version=1)
+    assert [g.shape for g in got] == [(1, 19, 256), (1, 24, 256), (1, 19, 256)]
+    for x, g in zip(xs, got):
+        np.testing.assert_array_equal(g, hub.encode(x[None], version=1))
+    with pytest.raises(ValueError):
+        hub.encode_batch([np.zeros((2, 6400), np.float32)])
