@@ -36,6 +36,7 @@ import numpy as np  # noqa: E402
 METRIC = "audio-sec synthesized/sec (10 s @40 kHz, 1 GPU) + HBM GB/s & MFMA util per op"
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 SR = 40000
 P_FRAMES = 1000           # 10 s at 100 frames/s
 CPU_SAMPLE_FRAMES = 400   # 4 s sample for the numpy baseline (about 10 s of CPU work)
@@ -46,6 +47,23 @@ def _log(msg):
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "synth_40k_resblock_traffic.md")
+
+
+def family_entry(t, peak_tflops=PEAK_FP32_TFLOPS):
+    """ms, TFLOP/s, GB/s of one timing family, and its roofline fraction
+    achieved / min(peak FLOP/s, AI x peak HBM bandwidth), AI = FLOPs / bytes."""
+    ms, fl, by = t["ms"], t["flops"], t["bytes"]
+    e = {"ms": round(ms, 4), "tflops": None, "gbs": None, "roof_frac": None}
+    if ms > 0:
+        tf = fl / (ms / 1e3) / 1e12
+        gbs = by / (ms / 1e3) / 1e9
+        e["tflops"], e["gbs"] = round(tf, 2), round(gbs, 1)
+        roof_tf = min(peak_tflops, (fl / by) * PEAK_HBM_GBS / 1e3) if by > 0 and fl > 0 else None
+        if roof_tf:
+            e["roof_frac"] = round(tf / roof_tf, 3)
+        elif by > 0:
+            e["roof_frac"] = round(gbs / PEAK_HBM_GBS, 3)
+    return e
 
 
 def profiled_traffic():
@@ -259,10 +277,106 @@ def _blas_threads():
         return 1
 
 
+def bench_bf16(args, precision):
+    """config 2 x 4 independent seeds as one batch of 4, with
+    the GeneratorNSF upsample ConvTranspose1d and the enc_p matmuls on bf16
+    MFMA, fp32 accumulate (precision 1); precision 2 also puts the decoder
+    ResBlocks on bf16 (reported separately).  The waveform SNR against the
+    fp32 path on the same inputs is measured in the same run (untimed)."""
+    import math
+
+    from rvc_hip import _hip, synthetic as syn
+    from rvc_hip.hip_ops import get_context
+    from rvc_hip.synth import HipSynthesizer
+
+    if not _hip.has_so:
+        raise RuntimeError(f"HIP backend missing: {_hip.so_load_error}")
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=0)
+    ctx = get_context()
+    s = HipSynthesizer(w, sr=geom.sr, ctx=ctx, precision=precision)
+    P, B = P_FRAMES, 4
+    ins = [syn.make_synth_inputs(geom, P, seed=sd) for sd in (41, 42, 43, 44)]
+    cat = {k: np.ascontiguousarray(np.concatenate([i[k] for i in ins], axis=0)) for k in
+           ("phone", "pitch", "nsff0", "sid", "nz", "ns")}
+    ids = {
+        "phone": ctx.upload(cat["phone"].astype(np.float32)),
+        "pitch": ctx.upload(cat["pitch"].astype(np.int64)),
+        "f0": ctx.upload(cat["nsff0"].astype(np.float32)),
+        "sid": ctx.upload(cat["sid"].astype(np.int64)),
+        "nz": ctx.upload(cat["nz"].astype(np.float32)),
+        "ns": ctx.upload(cat["ns"].astype(np.float32).reshape(-1)),
+    }
+    n_out = P * geom.upp
+    wave_id = ctx.alloc(B * n_out)
+
+    def step():
+        s.infer_dev(ids["phone"], ids["pitch"], ids["f0"], ids["sid"], ids["nz"], ids["ns"], B, P, wave_id)
+
+    for _ in range(args.warmup):
+        step()
+    s.set_timing("dec.rb")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = time.perf_counter() - t0
+    rb = s.get_timing()
+    s.set_timing("")
+    ms_step = dt * 1e3 / args.steps
+    audio_s = P / 100.0 * B
+    value = audio_s * args.steps / dt
+    _log(f"bench config 5 (precision {precision}): {ms_step:.3f} ms/step, {value:.1f} audio-s/s")
+    y = ctx.download(wave_id, (B, 1, n_out))
+
+    peak_rb = PEAK_BF16_TFLOPS if precision >= 2 else PEAK_FP32_TFLOPS
+    n_launch = max(rb["launches"], 1)
+    avg_s = rb["ms"] / 1e3 / n_launch
+    achieved = rb["flops"] / n_launch / avg_s / 1e12 if avg_s > 0 else 0.0
+    roofline = {"kernel": "conv1d_" + ("bf16" if precision >= 2 else "mfma") + " (GeneratorNSF ResBlock convs)",
+                "bound": "mfma", "achieved": round(achieved, 2), "peak": peak_rb, "unit": "TFLOP/s",
+                "frac": round(achieved / peak_rb, 4), "traffic": None,
+                "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n_launch // args.steps,
+                "share_of_step": round(rb["ms"] / (dt * 1e3), 3)}
+    breakdown = {}
+    for tag, peak in (("dec.rb", peak_rb), ("dec.ups", PEAK_BF16_TFLOPS), ("enc", PEAK_BF16_TFLOPS),
+                      ("flow", PEAK_FP32_TFLOPS)):
+        if args.quick:
+            break
+        s.set_timing(tag)
+        step()
+        breakdown[tag] = family_entry(s.get_timing(), peak)
+    s.set_timing("")
+    snr = None
+    if not args.quick:
+        ref = HipSynthesizer(w, sr=geom.sr, ctx=ctx, precision=0)
+        y0 = ref.infer_controlled(cat["phone"], cat["pitch"], cat["nsff0"], cat["sid"], cat["nz"], cat["ns"])
+        ref.close()
+        snr = min(10.0 * math.log10(float((y0[b].astype(np.float64) ** 2).sum()) /
+                                    max(float(((y[b].astype(np.float64) - y0[b]) ** 2).sum()), 1e-300))
+                  for b in range(B))
+    what = "ups + enc_p matmuls" if precision == 1 else "ups + enc_p matmuls + ResBlocks"
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 (" + what + "), f32 elsewhere; f32 accumulate",
+        "data": "synthetic (4 seeded inputs, random-init weights)",
+        "config": {"workload": f"config 5: config 2 x 4 seeds as batch 4, {what} on bf16 MFMA",
+                   "frames": P, "batch": B, "sample_rate": SR, "output_samples": n_out},
+        "roofline": roofline, "cpu_baseline": None,
+        "snr_db_vs_fp32": None if snr is None else round(snr, 2), "snr_bar_db": 40.0,
+        "breakdown": breakdown,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", default="synth40k", choices=("synth40k", "hubert", "dec48k-b8"),
-                    help="synth40k: BASELINE config 2 (default); hubert: config 3; dec48k-b8: config 4")
+    ap.add_argument("--workload", default="synth40k",
+                    choices=("synth40k", "hubert", "dec48k-b8", "synth40k-bf16-b4", "synth40k-bf16rb-b4"),
+                    help="synth40k: BASELINE config 2 (default); hubert: config 3; dec48k-b8: config 4; "
+                         "synth40k-bf16-b4: config 5 (ups + enc_p matmuls on bf16); synth40k-bf16rb-b4: config 5 "
+                         "with the ResBlocks on bf16 too (reported separately)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -284,6 +398,8 @@ def main():
         return bench_hubert(args)
     if args.workload == "dec48k-b8":
         return bench_dec48(args)
+    if args.workload.startswith("synth40k-bf16"):
+        return bench_bf16(args, precision=1 if args.workload == "synth40k-bf16-b4" else 2)
 
     from rvc_hip import _hip, synthetic as syn
     from rvc_hip.hip_ops import get_context
@@ -349,10 +465,7 @@ def main():
                 "dec.sine", "dec.pre", "enc", "flow"):
         s.set_timing(tag)
         step()
-        t = s.get_timing()
-        breakdown[tag] = {"ms": round(t["ms"], 4),
-                          "tflops": round(t["flops"] / (t["ms"] / 1e3) / 1e12, 2) if t["ms"] > 0 else None,
-                          "gbs": round(t["bytes"] / (t["ms"] / 1e3) / 1e9, 1) if t["ms"] > 0 else None}
+        breakdown[tag] = family_entry(s.get_timing())
     s.set_timing("")
 
     # PCIe-inclusive rate (host numpy in -> host numpy out); reported, never the headline

@@ -85,6 +85,16 @@ int32_t rvc_conv1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
 int32_t rvc_conv_t1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
                      int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t padding,
                      int64_t output_padding, int64_t dil);
+/* No reference counterpart: rvc_conv1d / rvc_conv_t1d computed on bf16 matrix cores with fp32
+ * accumulate (inputs and weights rounded to bf16, nearest even; products summed in fp32), for callers
+ * that accept bf16 rounding (the config-5 mixed-precision path).  conv1d: stride 1, K <= 11 and
+ * (K-1)*dil <= 64; conv_t1d: dilation 1, stride <= 16 and ceil(K/stride) <= 11.  Same arguments. */
+int32_t rvc_conv1d_bf16(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                        int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t pad_l, int64_t pad_r,
+                        int64_t dil);
+int32_t rvc_conv_t1d_bf16(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                          int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t padding,
+                          int64_t output_padding, int64_t dil);
 /* replaces rvc_embed (engine/src/ffi.zig:503): out[n,dim] = table[ids[n],:]; ids are int32,
  * validated by the caller (negative ids wrap once) */
 int32_t rvc_embed(int64_t h, int64_t ids, int64_t table, int64_t out, int64_t n, int64_t table_rows,
@@ -238,6 +248,10 @@ int32_t rvc_synth_decode_dev(int64_t s, int64_t z, int64_t f0, int64_t g, int64_
 /* Copy a named intermediate of the last run to the host (n floats): "enc_in",
  * "enc_out", "stats", "z_p", "z", "g", "har", "dec_pre", "dec_stage0".."dec_stage3". */
 int32_t rvc_synth_read(int64_t s, const char* name, float* dst, int64_t n);
+/* Before rvc_synth_finalize: 0 = fp32 (default); 1 = the GeneratorNSF upsample ConvTranspose1d and
+ * the enc_p matmuls (embedding linear, q/k/v, conv_o, FFN, proj) on bf16 MFMA with fp32 accumulate
+ * (BASELINE config 5); 2 = mode 1 plus the decoder ResBlock convs on bf16. */
+int32_t rvc_synth_set_precision(int64_t s, int32_t mode);
 /* Keep a copy of each decoder stage output ("dec_stage<i>") for rvc_synth_read. */
 int32_t rvc_synth_set_debug(int64_t s, int32_t keep_stages);
 /* Per-kernel-family timing with HIP events on the session stream.  tag selects

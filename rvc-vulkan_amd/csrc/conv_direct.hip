@@ -116,6 +116,36 @@ __global__ void pack_convt_phase_kernel(const float* w, float* out, int C_in, in
   out[idx] = co < C_out ? w[((long long)ci * C_out + co) * K + k] : 0.f;
 }
 
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// [C_out][C_in][K] fp32 -> [K][C_out][ldi] bf16; idx enumerates the destination
+__global__ void pack_conv_weight_bf16_kernel(const float* w, uint16_t* out, int C_out, int C_in, int K, int ldi) {
+  const long long n = (long long)K * C_out * ldi;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int ci = (int)(idx % ldi);
+  const int co = (int)((idx / ldi) % C_out);
+  const int k = (int)(idx / ((long long)ldi * C_out));
+  out[idx] = ci < C_in ? bf16_rne(w[((long long)co * C_in + ci) * K + k]) : (uint16_t)0;
+}
+
+// phase r of a ConvTranspose1d, [C_in][C_out][K] fp32 -> [J][C_out][ldi] bf16
+__global__ void pack_convt_phase_bf16_kernel(const float* w, uint16_t* out, int C_in, int C_out, int K, int st,
+                                             int r, int J, int ldi) {
+  const long long n = (long long)J * C_out * ldi;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n) return;
+  const int ci = (int)(idx % ldi);
+  const int co = (int)((idx / ldi) % C_out);
+  const int jp = (int)(idx / ((long long)ldi * C_out));
+  const int k = r + (J - 1 - jp) * st;
+  out[idx] = ci < C_in ? bf16_rne(w[((long long)ci * C_out + co) * K + k]) : (uint16_t)0;
+}
+
 unsigned grid1d(long long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -159,6 +189,24 @@ void launch_pack_convt_phase(const float* w, float* out, int C_in, int C_out, in
   hipLaunchKernelGGL(pack_convt_phase_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_in, C_out, K,
                      st, r, J, ld);
   check_launch("pack_convt_phase");
+}
+
+void launch_pack_conv_weight_bf16(const float* w, uint16_t* out, int C_out, int C_in, int K, hipStream_t s) {
+  const int ldi = bf16_ld(C_in);
+  const long long n = (long long)K * C_out * ldi;
+  if (n == 0) return;
+  hipLaunchKernelGGL(pack_conv_weight_bf16_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_out, C_in, K, ldi);
+  check_launch("pack_conv_weight_bf16");
+}
+
+void launch_pack_convt_phase_bf16(const float* w, uint16_t* out, int C_in, int C_out, int K, int st, int r, int J,
+                                  hipStream_t s) {
+  const int ldi = bf16_ld(C_in);
+  const long long n = (long long)J * C_out * ldi;
+  if (n == 0) return;
+  hipLaunchKernelGGL(pack_convt_phase_bf16_kernel, dim3(grid1d(n)), dim3(256), 0, s, w, out, C_in, C_out, K, st, r, J,
+                     ldi);
+  check_launch("pack_convt_phase_bf16");
 }
 
 }  // namespace rvc

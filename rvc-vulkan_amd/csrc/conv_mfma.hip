@@ -351,11 +351,7 @@ bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
   for (int g = 0; g < a.n_groups; ++g) RVC_CHECK(a.g[g].K <= KMAX, "conv1d_mfma: taps exceed the configuration");
   hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX>), grid, dim3(C::NT), lds, s, a);
   check_launch("conv1d_mfma");
-  if (a.ksplit > 1) {
-    const long long n = (long long)a.B * a.C_out * a.g[0].n_out;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
-    check_launch("splitk_reduce");
-  }
+  if (a.ksplit > 1) launch_splitk_reduce(a, s);
   return true;
 }
 
@@ -406,6 +402,13 @@ long long n_blocks(const ConvLaunch& a, int BM, int BN) {
 }
 
 }  // namespace
+
+void launch_splitk_reduce(const ConvLaunch& a, hipStream_t s) {
+  const long long n = (long long)a.B * a.C_out * a.g[0].n_out;
+  if (n <= 0) return;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  check_launch("splitk_reduce");
+}
 
 size_t conv1d_mfma_split_floats(const ConvLaunch& a) {
   const SplitPlan p = split_plan(a);

@@ -185,7 +185,7 @@ ConvLaunch one_conv(const float* x, long long C_in, long long L, const float* pa
 // (zero outside [0, L)), written into rows of length row_len.
 void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
                  long long C_in, long long L, long long C_out, long long K, long long stride, long long pad_l,
-                 long long dil, long long n_seg, long long lo_off, long long row_len) {
+                 long long dil, long long n_seg, long long lo_off, long long row_len, bool bf16 = false) {
   RVC_CHECK(n_seg >= 1 && lo_off >= 0 && lo_off + n_seg <= row_len, "conv1d: output segment outside the output row");
   check_i32(L, "conv1d"); check_i32(row_len, "conv1d"); check_i32(lo_off * stride + pad_l, "conv1d");
   check_i32(C_in * K, "conv1d"); check_i32(C_out, "conv1d");
@@ -193,9 +193,24 @@ void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, lon
   const float* wp = e.fptr(w, C_out * C_in * K, "conv1d w");
   const float* bp = b ? e.fptr(b, C_out, "conv1d bias") : nullptr;
   float* op = e.fptr(out, (B * C_out - 1) * row_len + lo_off + n_seg, "conv1d out");
+  if (bf16)
+    RVC_CHECK(stride == 1 && conv1d_bf16_supported((int)K, (int)dil),
+              "conv1d_bf16: stride 1, K <= " + std::to_string(kConvTapsMax) + " and (K-1)*dil <= " +
+                  std::to_string(kConvHaloMax) + " only");
   if (dry) return;
   const long long in_off = lo_off * stride - pad_l;
-  if ((stride == 1 || stride == 2) && conv1d_mfma_supported((int)K, (int)dil)) {
+  if (bf16) {
+    uint16_t* packed = static_cast<uint16_t*>(e.scratch_for(sizeof(uint16_t) * K * C_out * bf16_ld((int)C_in)));
+    launch_pack_conv_weight_bf16(wp, packed, (int)C_out, (int)C_in, (int)K, e.stream);
+    ConvLaunch a = one_conv(xp, C_in, L, nullptr, bp, op, C_out, n_seg, B, K, dil, pad_l, 1);
+    a.g[0].w16 = packed;
+    a.w16_ld = bf16_ld((int)C_in);
+    a.g[0].in_off = (int)in_off;
+    a.g[0].out_off = (int)lo_off;
+    a.ob = C_out * row_len;
+    a.oc = row_len;
+    launch_conv1d_bf16(a, e.stream);
+  } else if ((stride == 1 || stride == 2) && conv1d_mfma_supported((int)K, (int)dil)) {
     float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * packed_ld((int)C_out) * C_in * K));
     launch_pack_conv_weight(wp, packed, (int)C_out, (int)C_in, (int)K, e.stream);
     ConvLaunch a = one_conv(xp, C_in, L, packed, bp, op, C_out, n_seg, B, K, dil, pad_l, stride);
@@ -218,13 +233,13 @@ void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, lon
 
 void op_conv1d(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
                long long C_in, long long L, long long C_out, long long K, long long stride, long long pad_l,
-               long long pad_r, long long dil) {
+               long long pad_r, long long dil, bool bf16 = false) {
   RVC_CHECK(B >= 1 && C_in >= 1 && C_out >= 1 && K >= 1 && stride >= 1 && dil >= 1 && pad_l >= 0 &&
                 pad_r >= 0 && L >= 0,
             "conv1d: invalid parameters (stride/dilation>=1, padding>=0, K>=1)");
   const long long n_out = (L + pad_l + pad_r - dil * (K - 1) - 1) / stride + 1;
   RVC_CHECK(L + pad_l + pad_r - dil * (K - 1) - 1 >= 0 && n_out >= 1, "conv1d: empty output");
-  conv1d_core(e, dry, x, w, b, out, B, C_in, L, C_out, K, stride, pad_l, dil, n_out, 0, n_out);
+  conv1d_core(e, dry, x, w, b, out, B, C_in, L, C_out, K, stride, pad_l, dil, n_out, 0, n_out, bf16);
 }
 
 // engine/src/ffi.zig:703-751: the output segment [lo_off, lo_off + seg_len)
@@ -238,17 +253,11 @@ void op_conv1d_seg(Engine& e, bool dry, long long x, long long w, long long b, l
   conv1d_core(e, dry, x, w, b, out, B, C_in, L, C_out, K, stride, pad_l, dil, seg_len, lo_off, l_out_full);
 }
 
-}  // namespace
-
-// Polyphase ConvTranspose1d on the MFMA kernel (dilation 1): output o with
-// (o + padding) = m*stride + r only sees taps k = r + j*stride of input
-// m - j, so phase r is a stride-1 conv over m with J_r taps whose outputs land
-// at o = m*stride + r - padding.  All phases go into one grouped launch.
-// Shared by the op-level exports and the synthesis session.
-void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc, const float* const* w_phases,
-                     const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
-                     int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine, int o_lo,
-                     int x_shift) {
+// The grouped launch of a polyphase ConvTranspose1d (fp32 or bf16 phase weights).
+ConvLaunch convt_polyphase_launch(const float* x, long long xb, long long xc, const float* const* w_phases,
+                                  const uint16_t* const* w16_phases, const float* bias, float* out, long long ob,
+                                  long long oc, int B, int C_in, int C_out, int L, int n_out, int K, int stride,
+                                  int padding, int in_act, float in_slope, int combine, int o_lo, int x_shift) {
   RVC_CHECK(stride >= 1 && stride <= kMaxConvGroups, "conv_transpose1d: stride exceeds the grouped launch");
   ConvLaunch a{};
   a.xb = xb; a.xc = xc; a.ob = ob; a.oc = oc;
@@ -264,12 +273,40 @@ void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc,
     const int m1 = hi / stride;
     if (m1 < m0) continue;
     ConvGroup& g = a.g[a.n_groups++];
-    g.x = x; g.w = w_phases[r]; g.bias = bias; g.res = nullptr; g.out = out;
+    g.x = x; g.bias = bias; g.res = nullptr; g.out = out;
+    g.w = w_phases ? w_phases[r] : nullptr;
+    g.w16 = w16_phases ? w16_phases[r] : nullptr;
     g.K = J; g.dil = 1; g.in_off = m0 - (J > 0 ? J - 1 : 0) - x_shift;
     g.out_step = stride; g.out_off = m0 * stride + r - padding;
     g.n_out = m1 - m0 + 1; g.combine = combine;
   }
+  return a;
+}
+
+}  // namespace
+
+// Polyphase ConvTranspose1d on the MFMA kernel (dilation 1): output o with
+// (o + padding) = m*stride + r only sees taps k = r + j*stride of input
+// m - j, so phase r is a stride-1 conv over m with J_r taps whose outputs land
+// at o = m*stride + r - padding.  All phases go into one grouped launch.
+// Shared by the op-level exports and the synthesis session.
+void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc, const float* const* w_phases,
+                     const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
+                     int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine, int o_lo,
+                     int x_shift) {
+  const ConvLaunch a = convt_polyphase_launch(x, xb, xc, w_phases, nullptr, bias, out, ob, oc, B, C_in, C_out, L,
+                                              n_out, K, stride, padding, in_act, in_slope, combine, o_lo, x_shift);
   if (a.n_groups > 0) launch_conv1d_mfma(a, st);
+}
+
+void convt_polyphase_bf16(hipStream_t st, const float* x, long long xb, long long xc,
+                          const uint16_t* const* w16_phases, int w16_ld, const float* bias, float* out, long long ob,
+                          long long oc, int B, int C_in, int C_out, int L, int n_out, int K, int stride, int padding,
+                          int in_act, float in_slope, int combine) {
+  ConvLaunch a = convt_polyphase_launch(x, xb, xc, nullptr, w16_phases, bias, out, ob, oc, B, C_in, C_out, L, n_out,
+                                        K, stride, padding, in_act, in_slope, combine, 0, 0);
+  a.w16_ld = w16_ld;
+  if (a.n_groups > 0) launch_conv1d_bf16(a, st);
 }
 
 namespace {
@@ -282,7 +319,7 @@ namespace {
 void conv_t1d_core(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long vx,
                    long long vw, long long vb, long long vo, long long B, long long C_in, long long L, long long C_out,
                    long long K, long long stride, long long padding, long long dil, long long n_seg, long long lo_off,
-                   long long row_len, long long win_lo, long long win_len) {
+                   long long row_len, long long win_lo, long long win_len, bool bf16 = false) {
   RVC_CHECK(n_seg >= 1 && lo_off >= 0 && lo_off + n_seg <= row_len,
             "conv_transpose1d: output segment outside the output row");
   RVC_CHECK(win_lo >= 0 && win_len >= 1 && win_lo + win_len <= L,
@@ -293,9 +330,28 @@ void conv_t1d_core(Engine& e, bool dry, long long x, long long w, long long b, l
   const float* wp = fview(e, w, vw, C_in * C_out * K, "conv_t1d w");
   const float* bp = b ? fview(e, b, vb, C_out, "conv_t1d bias") : nullptr;
   float* op = fview(e, out, vo, (B * C_out - 1) * row_len + lo_off + n_seg, "conv_t1d out");
+  const bool poly = dil == 1 && stride <= kMaxConvGroups && (K + stride - 1) / stride <= kConvTapsMax;
+  if (bf16)
+    RVC_CHECK(poly && lo_off == 0 && n_seg == row_len && win_lo == 0 && win_len == L,
+              "conv_t1d_bf16: dilation 1, stride <= " + std::to_string(kMaxConvGroups) + " and ceil(K/stride) <= " +
+                  std::to_string(kConvTapsMax) + " only");
   if (dry) return;
   const int ld = packed_ld((int)C_out);
-  if (dil == 1 && stride <= kMaxConvGroups && (K + stride - 1) / stride <= kConvTapsMax) {
+  if (bf16) {
+    const int ldi = bf16_ld((int)C_in);
+    uint16_t* packed = static_cast<uint16_t*>(e.scratch_for(sizeof(uint16_t) * C_out * ldi * (K + stride)));
+    std::vector<const uint16_t*> phases(stride);
+    long long off = 0;
+    for (int r = 0; r < stride; ++r) {
+      const int J = convt_phase_taps((int)K, (int)stride, r);
+      launch_pack_convt_phase_bf16(wp, packed + off, (int)C_in, (int)C_out, (int)K, (int)stride, r, J, e.stream);
+      phases[r] = packed + off;
+      off += (long long)J * C_out * ldi;
+    }
+    convt_polyphase_bf16(e.stream, xp, C_in * L, L, phases.data(), ldi, bp, op, C_out * row_len, row_len, (int)B,
+                         (int)C_in, (int)C_out, (int)L, (int)n_seg, (int)K, (int)stride, (int)padding, ACT_NONE, 0.f,
+                         COMB_STORE);
+  } else if (poly) {
     // packed phases back to back in the scratch (16-byte aligned: ld % 4 == 0)
     float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * C_in * ld * (K + stride)));
     std::vector<const float*> phases(stride);
@@ -324,13 +380,14 @@ void conv_t1d_core(Engine& e, bool dry, long long x, long long w, long long b, l
 
 void op_conv_t1d(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
                  long long C_in, long long L, long long C_out, long long K, long long stride, long long padding,
-                 long long opad, long long dil) {
+                 long long opad, long long dil, bool bf16 = false) {
   RVC_CHECK(B >= 1 && C_in >= 1 && C_out >= 1 && K >= 1 && stride >= 1 && dil >= 1 && padding >= 0 &&
                 opad >= 0 && L >= 1,
             "conv_transpose1d: invalid parameters (stride/dilation>=1, padding/output_padding>=0)");
   const long long n_out = (L - 1) * stride - 2 * padding + dil * (K - 1) + opad + 1;
   RVC_CHECK(n_out >= 1, "conv_transpose1d: empty output");
-  conv_t1d_core(e, dry, x, w, b, out, 0, 0, 0, 0, B, C_in, L, C_out, K, stride, padding, dil, n_out, 0, n_out, 0, L);
+  conv_t1d_core(e, dry, x, w, b, out, 0, 0, 0, 0, B, C_in, L, C_out, K, stride, padding, dil, n_out, 0, n_out, 0, L,
+                bf16);
 }
 
 // engine/src/ffi.zig:636-701 (engine/src/engine.zig:2430-2468): output
@@ -764,6 +821,25 @@ int32_t rvc_conv1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
 int32_t rvc_conv_t1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t l,
                      int64_t c_out, int64_t k, int64_t stride, int64_t padding, int64_t output_padding, int64_t dil) {
   return single(h, 5, x, w, b, {B, c_in, l, c_out, k, stride, padding, output_padding, dil, out});
+}
+
+int32_t rvc_conv1d_bf16(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t l,
+                        int64_t c_out, int64_t k, int64_t stride, int64_t pad_l, int64_t pad_r, int64_t dil) {
+  return guarded(h, [&](Engine& e) {
+    op_conv1d(e, true, x, w, b, out, B, c_in, l, c_out, k, stride, pad_l, pad_r, dil, true);
+    submit(e, [&] { op_conv1d(e, false, x, w, b, out, B, c_in, l, c_out, k, stride, pad_l, pad_r, dil, true); });
+  });
+}
+
+int32_t rvc_conv_t1d_bf16(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                          int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t padding,
+                          int64_t output_padding, int64_t dil) {
+  return guarded(h, [&](Engine& e) {
+    op_conv_t1d(e, true, x, w, b, out, B, c_in, l, c_out, k, stride, padding, output_padding, dil, true);
+    submit(e, [&] {
+      op_conv_t1d(e, false, x, w, b, out, B, c_in, l, c_out, k, stride, padding, output_padding, dil, true);
+    });
+  });
 }
 
 int32_t rvc_embed(int64_t h, int64_t ids, int64_t table, int64_t out, int64_t n, int64_t table_rows,

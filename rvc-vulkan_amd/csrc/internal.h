@@ -10,6 +10,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -86,6 +87,7 @@ struct ConvGroup {
   int out_off;
   int n_out;
   int combine;
+  const uint16_t* w16;  // bf16 launches: weights [K][C_out][w16_ld] in bf16, 16-byte aligned
   int tiles;          // output tiles per workgroup (set by the launcher)
 };
 
@@ -100,6 +102,7 @@ struct ConvLaunch {
   const float* bias2; // second per-channel addend [B][C_out] or null
   long long bias2b;
   int C_in, C_out, w_ld, L_in, B;
+  int w16_ld;  // bf16 weight row length (C_in rounded up to 8, zero padded)
   int in_act;  float in_slope;
   int out_act; float out_slope;
   float div;
@@ -116,6 +119,29 @@ bool conv1d_mfma_supported(int K, int dil);
 // Scratch floats a launch needs for split-K partial sums (0: no split).
 size_t conv1d_mfma_split_floats(const ConvLaunch& a);
 void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s);
+// out = combine(act(sum of the split-K partials + bias ...)) for a launch
+// with a.ksplit > 1 (shared by the fp32 and bf16 kernels)
+void launch_splitk_reduce(const ConvLaunch& a, hipStream_t s);
+
+// The bf16 variant (v_mfma_f32_32x32x16_bf16, fp32 accumulate, input stride 1):
+// every group carries bf16 weights in g.w16 with row length a.w16_ld.
+bool conv1d_bf16_supported(int K, int dil);
+size_t conv1d_bf16_split_floats(const ConvLaunch& a);
+void launch_conv1d_bf16(const ConvLaunch& a, hipStream_t s);
+// bf16 weight row length for C_in input channels
+inline int bf16_ld(int C_in) { return (C_in + 7) / 8 * 8; }
+// device-side bf16 packers: [C_out][C_in][K] -> [K][C_out][bf16_ld(C_in)], and
+// ConvTranspose phase r: [C_in][C_out][K] -> [J][C_out][bf16_ld(C_in)]
+void launch_pack_conv_weight_bf16(const float* w, uint16_t* out, int C_out, int C_in, int K, hipStream_t s);
+void launch_pack_convt_phase_bf16(const float* w, uint16_t* out, int C_in, int C_out, int K, int st, int r, int J,
+                                  hipStream_t s);
+// float -> bf16 bits, round to nearest even (the device staging uses the same rule)
+inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
 
 // packed-weight leading dimension for C_out output channels
 inline int packed_ld(int c_out) { return (c_out + 3) / 4 * 4; }
@@ -161,6 +187,11 @@ void convt_polyphase(hipStream_t st, const float* x, long long xb, long long xc,
                      const float* bias, float* out, long long ob, long long oc, int B, int C_in, int C_out, int L,
                      int n_out, int K, int stride, int padding, int in_act, float in_slope, int combine,
                      int o_lo = 0, int x_shift = 0);
+// The same with bf16 phase weights ([J_r][C_out][w16_ld] per phase) on the bf16 kernel.
+void convt_polyphase_bf16(hipStream_t st, const float* x, long long xb, long long xc,
+                          const uint16_t* const* w16_phases, int w16_ld, const float* bias, float* out, long long ob,
+                          long long oc, int B, int C_in, int C_out, int L, int n_out, int K, int stride, int padding,
+                          int in_act, float in_slope, int combine);
 // (Segment form: only output columns [o_lo, n_out) are computed, and x's
 // column 0 is input column x_shift of the full row, L its window length.)
 // taps of phase r of a stride-st ConvTranspose with K taps

@@ -82,6 +82,24 @@ struct SessionBase {
     return o;
   }
 
+  // [C_out][C_in][K] -> bf16 [K][C_out][bf16_ld(C_in)], pad channels zero
+  static std::vector<uint16_t> pack_bf16(const std::vector<float>& w, long long C_out, long long C_in, long long K) {
+    const long long ld = bf16_ld((int)C_in);
+    std::vector<uint16_t> o((size_t)(K * C_out * ld), 0);
+    for (long long co = 0; co < C_out; ++co)
+      for (long long ci = 0; ci < C_in; ++ci)
+        for (long long k = 0; k < K; ++k) o[(k * C_out + co) * ld + ci] = f32_to_bf16(w[(co * C_in + ci) * K + k]);
+    return o;
+  }
+
+  uint16_t* upload16(const std::vector<uint16_t>& v) {
+    void* p = nullptr;
+    RVC_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 8) * sizeof(uint16_t)));
+    owned.push_back(p);
+    if (!v.empty()) RVC_HIP(hipMemcpy(p, v.data(), v.size() * sizeof(uint16_t), hipMemcpyHostToDevice));
+    return static_cast<uint16_t*>(p);
+  }
+
   float* upload(const std::vector<float>& v) {
     void* p = nullptr;
     RVC_HIP(hipMalloc(&p, std::max<size_t>(v.size(), 1) * sizeof(float)));
@@ -202,15 +220,27 @@ struct SessionBase {
       if (g.res) bytes += 4.0 * outs;
       if (g.combine != COMB_STORE) bytes += 4.0 * outs;
     }
-    const size_t need = conv1d_mfma_split_floats(a);
-    if (need == 0) {
-      run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(a, eng->stream); });
-      return;
-    }
+    const bool b16 = a.g[0].w16 != nullptr;
+    const size_t need = b16 ? conv1d_bf16_split_floats(a) : conv1d_mfma_split_floats(a);
     ConvLaunch sa = a;
-    sa.part = buf("splitk", need);
-    sa.part_floats = need;
-    run(t, 2.0 * mac, bytes, [&] { launch_conv1d_mfma(sa, eng->stream); });
+    if (need > 0) {
+      sa.part = buf("splitk", need);
+      sa.part_floats = need;
+    }
+    run(t, 2.0 * mac, bytes, [&] {
+      if (b16)
+        launch_conv1d_bf16(sa, eng->stream);
+      else
+        launch_conv1d_mfma(sa, eng->stream);
+    });
+  }
+  // the same launch on bf16 weights (row length bf16_ld(C_in)) when w16 is set
+  static ConvLaunch with16(ConvLaunch a, const uint16_t* w16) {
+    if (w16) {
+      a.g[0].w16 = w16;
+      a.w16_ld = bf16_ld(a.C_in);
+    }
+    return a;
   }
 };
 

@@ -19,6 +19,12 @@
 //   * conv_o / FFN conv_2 add the encoder residual in their epilogue; FFN
 //     conv_1 applies ReLU on store;
 //   * windowed relative-position attention is one kernel (attention.hip).
+//
+// Precision modes (rvc_synth_set_precision, before finalize): 0 = fp32
+// everywhere; 1 = the GeneratorNSF upsample ConvTranspose1d and the enc_p
+// matmuls (pitch/phone embedding linear, q/k/v, conv_o, FFN, proj) on bf16
+// MFMA with fp32 accumulate; 2 = mode 1 plus the
+// decoder ResBlock convs on bf16.  Everything else stays fp32.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -40,9 +46,12 @@ struct Synth : SessionBase {
   float *emb_phone_w = nullptr, *emb_phone_b = nullptr, *emb_pitch = nullptr, *emb_g = nullptr;
   struct EncL {
     float *wqkv, *bqkv, *wo, *bo, *ek, *ev, *g1, *b1, *w1, *bf1, *w2, *bf2, *g2, *b2;
+    uint16_t *wqkv16, *wo16, *w116, *w216;  // bf16 copies (precision >= 1), else null
   };
   std::vector<EncL> enc;
   float *proj_w = nullptr, *proj_b = nullptr;
+  uint16_t *emb_phone16 = nullptr, *proj16 = nullptr;
+  int precision = 0;
   struct FlowL {
     float *pre_w, *pre_b, *post_w, *post_b, *cond_w, *cond_b;
     float *in_w[kWnLayers], *in_b[kWnLayers], *rs_w[kWnLayers], *rs_b[kWnLayers];
@@ -57,6 +66,8 @@ struct Synth : SessionBase {
     float *nw, *nb;
     float* rw[3][2][3];
     float* rb[3][2][3];
+    std::vector<uint16_t*> phases16;  // precision >= 1
+    uint16_t* rw16[3][2][3];          // precision 2, else null
   };
   std::vector<StageW> stages;
 
@@ -85,18 +96,22 @@ struct Synth : SessionBase {
     return out;
   }
 
-  float* upload_conv(const std::string& key, long long C_out, long long C_in, long long K, bool wn) {
-    std::vector<float> w;
+  std::vector<float> conv_host(const std::string& key, long long C_out, long long C_in, long long K, bool wn) const {
     if (wn) {
-      w = deweight(key);
       const HostT& v = W(key + ".weight_v");
       check_shape(key + ".weight_v", v.shape, {C_out, C_in, K});
-    } else {
-      const HostT& t = W(key + ".weight");
-      check_shape(key + ".weight", t.shape, {C_out, C_in, K});
-      w = t.data;
+      return deweight(key);
     }
-    return upload(pack(w, C_out, C_in, K));
+    const HostT& t = W(key + ".weight");
+    check_shape(key + ".weight", t.shape, {C_out, C_in, K});
+    return t.data;
+  }
+  float* upload_conv(const std::string& key, long long C_out, long long C_in, long long K, bool wn) {
+    return upload(pack(conv_host(key, C_out, C_in, K, wn), C_out, C_in, K));
+  }
+  // bf16 copy of a conv weight when `on`, else null
+  uint16_t* upload_conv16(bool on, const std::string& key, long long C_out, long long C_in, long long K, bool wn) {
+    return on ? upload16(pack_bf16(conv_host(key, C_out, C_in, K, wn), C_out, C_in, K)) : nullptr;
   }
 
   void finalize(int sr_, const std::vector<int>& rates_, const std::vector<int>& kernels_) {
@@ -132,7 +147,9 @@ struct Synth : SessionBase {
 
     // ---- enc_p ----
     check_shape("enc_p.emb_phone.weight", ep.shape, {H, phone_dim});
+    const bool b16 = precision >= 1;
     emb_phone_w = upload(pack(ep.data, H, phone_dim, 1));
+    emb_phone16 = b16 ? upload16(pack_bf16(ep.data, H, phone_dim, 1)) : nullptr;
     emb_phone_b = upload_vec("enc_p.emb_phone.bias", H);
     check_shape("enc_p.emb_pitch.weight", W("enc_p.emb_pitch.weight").shape, {pitch_rows, H});
     emb_pitch = upload_key("enc_p.emb_pitch.weight");
@@ -150,6 +167,8 @@ struct Synth : SessionBase {
         bqkv.insert(bqkv.end(), b.data.begin(), b.data.end());
       }
       L.wqkv = upload(pack(qkv, 3 * H, H, 1));
+      L.wqkv16 = b16 ? upload16(pack_bf16(qkv, 3 * H, H, 1)) : nullptr;
+      L.wo16 = upload_conv16(b16, a + ".conv_o", H, H, 1, false);
       L.bqkv = upload(bqkv);
       L.wo = upload_conv(a + ".conv_o", H, H, 1, false);
       L.bo = upload_vec(a + ".conv_o.bias", H);
@@ -165,12 +184,15 @@ struct Synth : SessionBase {
       L.b2 = upload_vec(n2 + ".beta", H);
       const std::string f = "enc_p.encoder.ffn_layers." + std::to_string(i);
       L.w1 = upload_conv(f + ".conv_1", F, H, 3, false);
+      L.w116 = upload_conv16(b16, f + ".conv_1", F, H, 3, false);
+      L.w216 = upload_conv16(b16, f + ".conv_2", H, F, 3, false);
       L.bf1 = upload_vec(f + ".conv_1.bias", F);
       L.w2 = upload_conv(f + ".conv_2", H, F, 3, false);
       L.bf2 = upload_vec(f + ".conv_2.bias", H);
       enc.push_back(L);
     }
     proj_w = upload_conv("enc_p.proj", 2 * H, H, 1, false);
+    proj16 = upload_conv16(b16, "enc_p.proj", 2 * H, H, 1, false);
     proj_b = upload_vec("enc_p.proj.bias", 2 * H);
 
     // ---- flow ----
@@ -231,6 +253,17 @@ struct Synth : SessionBase {
               ph[((size_t)jp * c_in + ci) * ld + co] = wt[((size_t)ci * c + co) * K + k];
         }
         S.phases.push_back(upload(ph));
+        if (b16) {
+          const int ld16 = bf16_ld(c_in);
+          std::vector<uint16_t> p16((size_t)J * c * ld16, 0);
+          for (int jp = 0; jp < J; ++jp) {
+            const int k = r + (J - 1 - jp) * st;
+            for (int co = 0; co < c; ++co)
+              for (int ci = 0; ci < c_in; ++ci)
+                p16[((size_t)jp * c + co) * ld16 + ci] = f32_to_bf16(wt[((size_t)ci * c + co) * K + k]);
+          }
+          S.phases16.push_back(upload16(p16));
+        }
       }
       S.up_b = upload_vec(up + ".bias", c);
       const std::string nc = "dec.noise_convs." + std::to_string(i);
@@ -248,6 +281,7 @@ struct Synth : SessionBase {
             const std::string rb = "dec.resblocks." + std::to_string(3 * i + j) + (l == 0 ? ".convs1." : ".convs2.") +
                                    std::to_string(g);
             S.rw[j][l][g] = upload_conv(rb, c, c, ks[j], true);
+            S.rw16[j][l][g] = upload_conv16(precision >= 2, rb, c, c, ks[j], true);
             S.rb[j][l][g] = upload_vec(rb + ".bias", c);
           }
       stages.push_back(S);
@@ -280,7 +314,8 @@ struct Synth : SessionBase {
     float* phT = buf("phT", (size_t)B * phone_dim * P);
     launch_transpose(phone, phT, B, P, phone_dim, 1.0f, s);
     float* E = buf("encE", (size_t)B * HP);
-    conv("enc.embed", c1x1(phT, (long long)phone_dim * P, emb_phone_w, emb_phone_b, E, B, phone_dim, H, P));
+    conv("enc.embed", with16(c1x1(phT, (long long)phone_dim * P, emb_phone_w, emb_phone_b, E, B, phone_dim, H, P),
+                             emb_phone16));
     float* xin = buf("enc_in", (size_t)B * HP);
     launch_embed_combine(E, pitch, emb_pitch, pitch_rows, xin, B, H, P, (float)std::sqrt((double)H), 0.1f, s);
     float* xo = buf("enc_out", (size_t)B * HP);
@@ -292,24 +327,24 @@ struct Synth : SessionBase {
     const float* x = xin;
     for (int i = 0; i < n_layers; ++i) {
       const EncL& L = enc[i];
-      conv("enc.qkv", c1x1(x, HP, L.wqkv, L.bqkv, qkv, B, H, 3 * H, P));
+      conv("enc.qkv", with16(c1x1(x, HP, L.wqkv, L.bqkv, qkv, B, H, 3 * H, P), L.wqkv16));
       run("enc.attn", 4.0 * B * heads * (double)P * P * kc, 4.0 * B * 4 * HP,
           [&] { launch_relpos_attention(qkv, L.ek, L.ev, att, apart, B, heads, kc, P, kWindow, s); });
-      ConvLaunch co = c1x1(att, HP, L.wo, L.bo, o, B, H, H, P);
+      ConvLaunch co = with16(c1x1(att, HP, L.wo, L.bo, o, B, H, H, P), L.wo16);
       co.g[0].res = x; co.rb = HP; co.rc = P;
       conv("enc.o", co);
       run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g1, L.b1, xo, B, H, P, 1e-5f, s); });
-      ConvLaunch c1 = cargs_same(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
+      ConvLaunch c1 = with16(cargs_same(xo, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1), L.w116);
       c1.out_act = ACT_RELU;
       conv("enc.ffn", c1);
-      ConvLaunch c2 = cargs_same(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
+      ConvLaunch c2 = with16(cargs_same(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1), L.w216);
       c2.g[0].res = xo; c2.rb = HP; c2.rc = P;
       conv("enc.ffn", c2);
       run("enc.ln", 8.0 * B * HP, 8.0 * B * HP, [&] { launch_layernorm_cols(o, L.g2, L.b2, xo, B, H, P, 1e-5f, s); });
       x = xo;
     }
     float* st = buf("stats", (size_t)B * 2 * HP);
-    conv("enc.proj", c1x1(x, HP, proj_w, proj_b, st, B, H, 2 * H, P));
+    conv("enc.proj", with16(c1x1(x, HP, proj_w, proj_b, st, B, H, 2 * H, P), proj16));
     float* zp = buf("z_p", (size_t)B * HP);
     launch_zp(st, nz, zp, B, H, P, 0.66666f, s);
 
@@ -403,8 +438,14 @@ struct Synth : SessionBase {
         std::snprintf(tg, sizeof tg, "dec.ups.s%d", i);
         run(tg, 2.0 * B * (double)c_in * C * K * L, 4.0 * B * ((double)c_in * L + 2.0 * CL) + 4.0 * c_in * C * K,
             [&] {
-              convt_polyphase(s, cur, (long long)c_in * L, L, ph.data(), stages[i].up_b, X, CL, Lo, B, c_in, C, L, Lo,
-                              K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
+              if (!stages[i].phases16.empty()) {
+                std::vector<const uint16_t*> p16(stages[i].phases16.begin(), stages[i].phases16.end());
+                convt_polyphase_bf16(s, cur, (long long)c_in * L, L, p16.data(), bf16_ld(c_in), stages[i].up_b, X, CL,
+                                     Lo, B, c_in, C, L, Lo, K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
+              } else {
+                convt_polyphase(s, cur, (long long)c_in * L, L, ph.data(), stages[i].up_b, X, CL, Lo, B, c_in, C, L, Lo,
+                                K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
+              }
             });
       }
       // three ResBlock1 (k = 3, 7, 11) run side by side: each conv launch
@@ -434,7 +475,10 @@ struct Synth : SessionBase {
           g1.out_off = g2.out_off = 0;
           g1.n_out = g2.n_out = Lo;
           g1.combine = g2.combine = COMB_STORE;
+          g1.w16 = stages[i].rw16[j][0][gi];
+          g2.w16 = stages[i].rw16[j][1][gi];
         }
+        if (c1.g[0].w16) c1.w16_ld = c2.w16_ld = bf16_ld(C);
         conv(tg, c1);
         conv(tg, c2);
       }
@@ -650,6 +694,14 @@ int32_t rvc_synth_read(int64_t sh, const char* name, float* dst, int64_t n) {
   return sguard(sh, [&](Synth& s) {
     RVC_CHECK(name && dst && n >= 0, "read: invalid arguments");
     s.read(std::strcmp(name, "z") == 0 ? s.z_name : std::string(name), dst, n);
+  });
+}
+
+int32_t rvc_synth_set_precision(int64_t sh, int32_t mode) {
+  return sguard(sh, [&](Synth& s) {
+    RVC_CHECK(!s.ready, "set_precision: the session is already finalized");
+    RVC_CHECK(mode >= 0 && mode <= 2, "set_precision: mode must be 0 (fp32), 1 (bf16 ups + enc_p) or 2 (1 + ResBlocks)");
+    s.precision = mode;
   });
 }
 

@@ -63,6 +63,8 @@ SYMBOLS = {
     "rvc_relu": (I32, [I64] * 3),
     "rvc_conv1d": (I32, [I64] * 14),
     "rvc_conv_t1d": (I32, [I64] * 14),
+    "rvc_conv1d_bf16": (I32, [I64] * 14),
+    "rvc_conv_t1d_bf16": (I32, [I64] * 14),
     "rvc_embed": (I32, [I64] * 7),
     "rvc_add_inplace": (I32, [I64] * 4),
     "rvc_mul_inplace": (I32, [I64] * 4),
@@ -112,6 +114,7 @@ SYMBOLS = {
     "rvc_synth_decode": (I32, [I64, F32P, F32P, F32P, F32P, I64, I64, F32P]),
     "rvc_synth_decode_dev": (I32, [I64] * 8),
     "rvc_synth_read": (I32, [I64, CHARP, F32P, I64]),
+    "rvc_synth_set_precision": (I32, [I64, I32]),
     "rvc_synth_set_debug": (I32, [I64, I32]),
     "rvc_synth_set_timing": (I32, [I64, CHARP]),
     "rvc_synth_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL),

@@ -39,9 +39,7 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + sorted(glob.glob(os.path.join(CSRC, "*.cpp")))
 
 
-def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, "-o", tmp, *sources()]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -51,6 +49,25 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs[-60:]))
     if verbose and msgs:
         print("\n".join(msgs))
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every source to an object in parallel (a temporary folder),
+    then link the shared library."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="rvc_hip_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.basename(src) + ".o") for src in srcs]
+        with ThreadPoolExecutor(jobs) as ex:
+            for f in [ex.submit(_run, [hipcc(), *compile_flags, "-c", src, "-o", obj], verbose)
+                      for src, obj in zip(srcs, objs)]:
+                f.result()
+        tmp = OUT + ".tmp"
+        _run([hipcc(), "--offload-arch=gfx950", "-fPIC", "-shared", "-o", tmp, *objs], verbose)
     os.replace(tmp, OUT)
     return OUT
 

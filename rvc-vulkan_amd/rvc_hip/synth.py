@@ -47,11 +47,13 @@ class HipSynthesizer:
     """RVC v2 synthesizer with every weight resident on one MI355X."""
 
     def __init__(self, w: dict, config=None, sr: int | None = None, ctx: HipContext | None = None,
-                 geometry=None):
+                 geometry=None, precision: int = 0):
         """``config`` / ``sr`` derive the geometry like the reference's
         ``VitsConfig``; ``geometry`` (any object with ``upsample_rates``,
         ``upsample_kernels`` and ``sr``, e.g. a reference ``VitsConfig``)
-        overrides those three."""
+        overrides those three.  ``precision``: 0 fp32 (default); 1 the
+        upsample ConvTranspose1d and the enc_p matmuls on bf16 MFMA with fp32
+        accumulate; 2 also the decoder ResBlock convs."""
         self.cfg = VitsConfig(w, config, sr=sr)
         if geometry is not None:
             self.cfg.upsample_rates = [int(r) for r in geometry.upsample_rates]
@@ -65,6 +67,8 @@ class HipSynthesizer:
         if self.handle < 0:
             raise RuntimeError(f"rvc_synth_create failed: {_hip.last_error()}")
         self._w = w
+        self.precision = int(precision)
+        _hip._check(self._lib.rvc_synth_set_precision(self.handle, self.precision), "rvc_synth_set_precision")
         for key, arr in w.items():
             a = _f32(arr)
             shape = (ctypes.c_int64 * max(a.ndim, 1))(*(a.shape if a.ndim else (1,)))
