@@ -102,14 +102,15 @@ def register_session_backend(api, base_cls):
     return cls
 
 
-def bind_synthesizer(trn, ctx=None):
+def bind_synthesizer(trn, ctx=None, precision=0):
     """A ``HipSynthesizer`` holding the weights of a constructed reference
     ``SynthesizerTrn``: weights from ``trn.weight_dict``, upsample rates /
     kernels and sample rate from ``trn.cfg`` (``runtime/models/vits.py
-    :2245-2266``), so both sides use the same geometry."""
+    :2245-2266``), so both sides use the same geometry.  ``precision`` 1 / 2
+    selects the bf16 modes (config 5; with the ResBlocks)."""
     from .synth import HipSynthesizer
 
-    return HipSynthesizer(trn.weight_dict, geometry=trn.cfg, ctx=ctx)
+    return HipSynthesizer(trn.weight_dict, geometry=trn.cfg, ctx=ctx, precision=precision)
 
 
 def bind_hubert(encoder, ctx=None):
