@@ -135,11 +135,13 @@ def test_bind_synthesizer_uses_reference_geometry(monkeypatch):
     seen = {}
 
     class FakeSynth:
-        def __init__(self, w, config=None, sr=None, ctx=None, geometry=None):
-            seen.update(w=w, geometry=geometry, ctx=ctx)
+        def __init__(self, w, config=None, sr=None, ctx=None, geometry=None, precision=0):
+            seen.update(w=w, geometry=geometry, ctx=ctx, precision=precision)
 
     monkeypatch.setattr(synth, "HipSynthesizer", FakeSynth)
     cfg = types.SimpleNamespace(upsample_rates=[12, 10, 2, 2], upsample_kernels=[24, 20, 4, 4], sr=48000)
     trn = types.SimpleNamespace(weight_dict={"k": 1}, cfg=cfg)
     backend_hip.bind_synthesizer(trn)
-    assert seen["w"] == {"k": 1} and seen["geometry"] is cfg
+    assert seen["w"] == {"k": 1} and seen["geometry"] is cfg and seen["precision"] == 0
+    backend_hip.bind_synthesizer(trn, precision=1)
+    assert seen["precision"] == 1
