@@ -9,7 +9,12 @@
 //     halo is loaded once per chunk instead of K times, and
 //   * the packed weights W[0:K][ci0:ci0+BK*SK][co0:co0+BM] (float4 loads).
 // The next chunk's global loads are issued into registers before the MFMAs
-// of the current chunk, so their latency hides behind the matrix work.
+// of the current chunk, so their latency hides behind the matrix work; each
+// thread's staging offsets and padding masks are computed once per tile and
+// the masks applied when the registers are stored to LDS, so no wait for
+// those loads sits in front of the MFMAs.  Inside a chunk the LDS operands of
+// step s+1 are read before the MFMAs of step s are issued (two register sets,
+// ordered with sched_group_barrier).
 //
 // Each wave computes a WM x WN sub-tile with (WM/32)*(WN/32) 32x32
 // accumulators.  With SK > 1 the SK waves that share a sub-tile split the
@@ -21,12 +26,13 @@
 // and the 16 accumulator registers r of lane l hold
 //   row = (r%4) + 4*(l/32) + 8*(r/4), col = l%32.
 //
-// The fused epilogue: bias (and an optional second per-channel term), an
-// optional residual and, for an accumulating launch without activation, the
-// current output are the accumulators' starting values (loaded while the
-// first chunk stages); at the end leaky-ReLU / ReLU / tanh / GELU is applied
-// and the result combined into the output (store, accumulate, or
-// accumulate-then-divide).  Output position
+// The fused epilogue: the accumulators start from bias (and an optional
+// second per-channel term); a residual and, for an accumulating launch
+// without activation, the current output are loaded into registers right
+// after the first chunk's loads (the RES instantiation, chosen when a group
+// has either; the first staging does not wait for them) and added at the
+// end; then leaky-ReLU / ReLU / tanh / GELU is applied and the result combined
+// into the output (store, accumulate, or accumulate-then-divide).  Output position
 // i is written at i*out_step + out_off, which lets one phase of a polyphase
 // ConvTranspose1d use the same kernel.  A launch may carry up to
 // kMaxConvGroups independent convolutions with the same channel counts
@@ -80,7 +86,7 @@ struct Cfg {
 // without the cap the compiler spends registers on the accumulator-start
 // loads and drops the 128 x 128 tile to one wave per SIMD (measured 30 %
 // slower).
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX, bool RES>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64)
 __attribute__((amdgpu_waves_per_eu(KMAX == 1 ? 1 : 2)))
 void conv1d_mfma_kernel(ConvLaunch a) {
@@ -92,7 +98,7 @@ void conv1d_mfma_kernel(ConvLaunch a) {
   const int b = blockIdx.z % a.B;
   const int gi = (blockIdx.z / a.B) % a.n_groups;
   const int ks = blockIdx.z / (a.B * a.n_groups);  // channel split of a split-K launch
-  const ConvGroup& G = a.g[gi];
+  const ConvGroup G = a.g[gi];                      // one set of scalar loads
   const int i0 = blockIdx.x * BN;
   // input channels of this workgroup: all, or one split of a.ksplit
   const int csplit = a.ksplit > 1 ? a.csplit : a.C_in;
@@ -127,12 +133,6 @@ void conv1d_mfma_kernel(ConvLaunch a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.f;
 
-  // The accumulation starts from bias (+ the second per-channel term)
-  // (+ the residual) (+ the current output of an accumulating launch without
-  // activation).  These loads are issued with the first chunk's, so their
-  // latency hides behind its staging instead of stalling the epilogue.
-  // Split-K partials stay raw; with intra-workgroup split-K only the waves
-  // that run the epilogue (wk == 0) start from them.
   const bool fold_out = G.combine == COMB_ADD && a.out_act == ACT_NONE;
   const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
   float* ob = G.out + (long long)b * a.ob;
@@ -151,50 +151,71 @@ void conv1d_mfma_kernel(ConvLaunch a) {
           if (co >= a.C_out) continue;
           float v = G.bias ? G.bias[co] : 0.f;
           if (bias2) v = v + bias2[co];
-          if (rb) v = v + rb[co * a.rc + t];
-          if (fold_out) v = v + ob[co * a.oc + t];
           acc[m][n][r] = v;
         }
       }
   }
 
-  float xr[XPT];
-  float4 wreg[WPT];
+  // Staging map, fixed across chunks: element e of this thread stages x row
+  // xr_[e] (channel within the chunk) at window column j -> global offset
+  // xo[e] = xr_[e]*xc + t from the chunk's first channel (-1: padding), and
+  // weight vector e -> offset wo[e] from the chunk's first channel row.
   const int nx = BKT * XW;
   const int nw4 = K * BKT * W4ROW;
   const int tbase = i0 * S + G.in_off;
+  int xo[XPT], xr_[XPT];
+#pragma unroll
+  for (int e = 0; e < XPT; ++e) {
+    const int idx = tid + e * NT;
+    const int r = idx / XW;
+    const int j = idx - r * XW;
+    const int t = tbase + j;
+    const bool ok = idx < nx && t >= 0 && t < a.L_in;
+    xr_[e] = ok ? r : 1 << 30;
+    xo[e] = ok ? (int)((long long)r * a.xc + t) : 0;
+  }
+  int wo[WPT], wr_[WPT];
+#pragma unroll
+  for (int e = 0; e < WPT; ++e) {
+    const int idx = tid + e * NT;
+    const int row = idx / W4ROW;
+    const int c4 = idx - row * W4ROW;
+    const int k = row / BKT;
+    const int rr = row - k * BKT;
+    const bool ok = idx < nw4 && co0 + 4 * c4 < a.w_ld;
+    wr_[e] = ok ? rr : 1 << 30;
+    wo[e] = ok ? (k * a.C_in + rr) * a.w_ld + co0 + 4 * c4 : 0;
+  }
 
+  float xv[XPT];
+  float4 wreg[WPT];
+  float radd[RES ? TM : 1][RES ? TN : 1][16];
+  if constexpr (RES) {
+#pragma unroll
+    for (int m = 0; m < TM; ++m)
+#pragma unroll
+      for (int n = 0; n < TN; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) radd[m][n][r] = 0.f;
+  }
+  // gload only issues the loads (masked elements read a valid dummy address);
+  // the masks are applied by lstore, after the MFMAs that hide the latency.
   auto gload = [&](int ci0) {
+    const float* xc0 = xb + (long long)ci0 * a.xc;
+    const float* wc0 = G.w + (long long)ci0 * a.w_ld;
+    const int lim = ci_hi - ci0;
 #pragma unroll
-    for (int e = 0; e < XPT; ++e) {
-      const int idx = tid + e * NT;
-      const int r = idx / XW;
-      const int j = idx - r * XW;
-      const int ci = ci0 + r;
-      const int t = tbase + j;
-      float v = 0.f;
-      if (idx < nx && ci < ci_hi && t >= 0 && t < a.L_in) v = xb[(long long)ci * a.xc + t];
-      xr[e] = v;
-    }
+    for (int e = 0; e < XPT; ++e) xv[e] = xc0[xr_[e] < lim ? xo[e] : 0];
 #pragma unroll
-    for (int e = 0; e < WPT; ++e) {
-      const int idx = tid + e * NT;
-      const int row = idx / W4ROW;
-      const int c4 = idx - row * W4ROW;
-      const int k = row / BKT;
-      const int ci = ci0 + (row - k * BKT);
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (idx < nw4 && ci < ci_hi && co0 + 4 * c4 < a.w_ld)
-        v = *reinterpret_cast<const float4*>(G.w + ((long long)k * a.C_in + ci) * a.w_ld + co0 + 4 * c4);
-      wreg[e] = v;
-    }
+    for (int e = 0; e < WPT; ++e) wreg[e] = *reinterpret_cast<const float4*>(wc0 + (wr_[e] < lim ? wo[e] : 0));
   };
-  auto lstore = [&]() {
+  auto lstore = [&](int ci0) {
+    const int lim = ci_hi - ci0;
 #pragma unroll
     for (int e = 0; e < XPT; ++e) {
       const int idx = tid + e * NT;
       if (idx < nx) {
-        float v = xr[e];
+        float v = xr_[e] < lim ? xv[e] : 0.f;
         if (a.in_act == ACT_LEAKY) v = v >= 0.f ? v : v * a.in_slope;
         xs[idx] = v;
       }
@@ -202,36 +223,76 @@ void conv1d_mfma_kernel(ConvLaunch a) {
 #pragma unroll
     for (int e = 0; e < WPT; ++e) {
       const int idx = tid + e * NT;
-      if (idx < nw4) reinterpret_cast<float4*>(ws)[idx] = wreg[e];
+      if (idx < nw4) reinterpret_cast<float4*>(ws)[idx] = wr_[e] < lim ? wreg[e] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
 
   if (K > 0 && ci_hi > ci_lo) {
     const int nchunk = (ci_hi - ci_lo + BKT - 1) / BKT;
     gload(ci_lo);
+    // residual / accumulate target, issued after the first chunk's loads so
+    // the first staging does not wait for them; added in the epilogue
+    if (RES && a.ksplit <= 1 && wk == 0) {
+#pragma unroll
+      for (int m = 0; m < TM; ++m)
+#pragma unroll
+        for (int n = 0; n < TN; ++n) {
+          const int i = min(i0 + wn * WN + n * 32 + l32, G.n_out - 1);
+          const long long t = (long long)i * G.out_step + G.out_off;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int co = min(co0 + wm * WM + m * 32 + (r & 3) + 4 * half + 8 * (r >> 2), a.C_out - 1);
+            float v = 0.f;
+            if (rb) v = rb[co * a.rc + t];
+            if (fold_out) v = v + ob[co * a.oc + t];
+            radd[m][n][r] = v;
+          }
+        }
+    }
+    lstore(ci_lo);
+    __syncthreads();
     for (int c = 0; c < nchunk; ++c) {
-      lstore();
-      __syncthreads();
-      if (c + 1 < nchunk) gload(ci_lo + (c + 1) * BKT);
+      const bool more = c + 1 < nchunk;
+      const int cn = ci_lo + (c + 1) * BKT;
+      if (more) gload(cn);
+      // software-pipelined: the LDS operands of step s+1 are read before the
+      // MFMAs of step s are issued (two register sets, chosen by step parity)
+      const float* wbase = ws + (wk * BK + half) * BM + wm * WM + l32;
+      const float* xbase = xs + (wk * BK + half) * XW + (wn * WN + l32) * S;
+      float av[2][TM], bv[2][TN];
+      auto lda = [&](int k, int q, int p) {
+        const float* w_ = wbase + (k * BKT + 2 * q) * BM;
+        const float* x_ = xbase + 2 * q * XW + k * dil;
+#pragma unroll
+        for (int m = 0; m < TM; ++m) av[p][m] = w_[m * 32];
+#pragma unroll
+        for (int n = 0; n < TN; ++n) bv[p][n] = x_[n * 32 * S];
+      };
+      static_assert((BK / 2) % 2 == 0 || BK == 2, "step parity must repeat per tap");
+      lda(0, 0, 0);
       for (int k = 0; k < K; ++k) {
-        const float* wk_ = ws + (k * BKT + wk * BK) * BM + wm * WM + l32;
-        const float* xk = xs + wk * BK * XW + (wn * WN + l32) * S + k * dil;
 #pragma unroll
         for (int q = 0; q < BK / 2; ++q) {
-          const int r = 2 * q + half;
-          float av[TM], bv[TN];
-#pragma unroll
-          for (int m = 0; m < TM; ++m) av[m] = wk_[r * BM + m * 32];
-#pragma unroll
-          for (int n = 0; n < TN; ++n) bv[n] = xk[r * XW + n * 32 * S];
+          const int p = q & 1;
+          if (q + 1 < BK / 2)
+            lda(k, q + 1, p ^ 1);
+          else
+            lda(k + 1 < K ? k + 1 : k, 0, p ^ 1);  // last tap: a harmless re-read, no branch
 #pragma unroll
           for (int m = 0; m < TM; ++m)
 #pragma unroll
             for (int n = 0; n < TN; ++n)
-              acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[m], bv[n], acc[m][n], 0, 0, 0);
+              acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p][m], bv[p][n], acc[m][n], 0, 0, 0);
+          // keep the next step's LDS reads ahead of this step's MFMAs
+          __builtin_amdgcn_sched_group_barrier(0x100, (TM + 1) / 2 + (TN + 1) / 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
         }
       }
       __syncthreads();
+      if (more) {
+        lstore(cn);
+        __syncthreads();
+      }
     }
   }
 
@@ -294,7 +355,9 @@ void conv1d_mfma_kernel(ConvLaunch a) {
         const int row = (r & 3) + 4 * half + 8 * (r >> 2);
         const int co = co0 + wm * WM + m * 32 + row;
         if (co >= a.C_out) continue;
-        float v = apply_act(acc[m][n][r], a.out_act, a.out_slope);
+        float v = acc[m][n][r];
+        if constexpr (RES) v = v + radd[m][n][r];
+        v = apply_act(v, a.out_act, a.out_slope);
         float* o = ob + co * a.oc + t;
         if (G.combine == COMB_ADD && !fold_out) {
           v = *o + v;
@@ -349,7 +412,15 @@ bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
   if (lds > kLdsLimit) return false;
   dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B * std::max(a.ksplit, 1));
   for (int g = 0; g < a.n_groups; ++g) RVC_CHECK(a.g[g].K <= KMAX, "conv1d_mfma: taps exceed the configuration");
-  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX>), grid, dim3(C::NT), lds, s, a);
+  // launches with a residual or an accumulate target (folded into the result
+  // in the epilogue) take the instantiation that prefetches them
+  bool res = false;
+  for (int g = 0; g < a.n_groups; ++g)
+    res |= a.g[g].res != nullptr || (a.g[g].combine == COMB_ADD && a.out_act == ACT_NONE);
+  if (res && a.ksplit <= 1)
+    hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX, true>), grid, dim3(C::NT), lds, s, a);
+  else
+    hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX, false>), grid, dim3(C::NT), lds, s, a);
   check_launch("conv1d_mfma");
   if (a.ksplit > 1) launch_splitk_reduce(a, s);
   return true;
