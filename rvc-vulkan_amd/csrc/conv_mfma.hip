@@ -26,13 +26,12 @@
 // and the 16 accumulator registers r of lane l hold
 //   row = (r%4) + 4*(l/32) + 8*(r/4), col = l%32.
 //
-// The fused epilogue: the accumulators start from bias (and an optional
-// second per-channel term); a residual and, for an accumulating launch
-// without activation, the current output are loaded into registers right
-// after the first chunk's loads (the RES instantiation, chosen when a group
-// has either; the first staging does not wait for them) and added at the
-// end; then leaky-ReLU / ReLU / tanh / GELU is applied and the result combined
-// into the output (store, accumulate, or accumulate-then-divide).  Output position
+// The fused epilogue: bias (and an optional second per-channel term), an
+// optional residual and, for an accumulating launch without activation, the
+// current output are the accumulators' starting values (loaded while the
+// first chunk stages); at the end leaky-ReLU / ReLU / tanh / GELU is applied
+// and the result combined into the output (store, accumulate, or
+// accumulate-then-divide).  Output position
 // i is written at i*out_step + out_off, which lets one phase of a polyphase
 // ConvTranspose1d use the same kernel.  A launch may carry up to
 // kMaxConvGroups independent convolutions with the same channel counts
@@ -86,7 +85,7 @@ struct Cfg {
 // without the cap the compiler spends registers on the accumulator-start
 // loads and drops the 128 x 128 tile to one wave per SIMD (measured 30 %
 // slower).
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX, bool RES>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64)
 __attribute__((amdgpu_waves_per_eu(KMAX == 1 ? 1 : 2)))
 void conv1d_mfma_kernel(ConvLaunch a) {
@@ -151,6 +150,8 @@ void conv1d_mfma_kernel(ConvLaunch a) {
           if (co >= a.C_out) continue;
           float v = G.bias ? G.bias[co] : 0.f;
           if (bias2) v = v + bias2[co];
+          if (rb) v = v + rb[co * a.rc + t];
+          if (fold_out) v = v + ob[co * a.oc + t];
           acc[m][n][r] = v;
         }
       }
@@ -189,15 +190,6 @@ void conv1d_mfma_kernel(ConvLaunch a) {
 
   float xv[XPT];
   float4 wreg[WPT];
-  float radd[RES ? TM : 1][RES ? TN : 1][16];
-  if constexpr (RES) {
-#pragma unroll
-    for (int m = 0; m < TM; ++m)
-#pragma unroll
-      for (int n = 0; n < TN; ++n)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) radd[m][n][r] = 0.f;
-  }
   // gload only issues the loads (masked elements read a valid dummy address);
   // the masks are applied by lstore, after the MFMAs that hide the latency.
   auto gload = [&](int ci0) {
@@ -230,25 +222,6 @@ void conv1d_mfma_kernel(ConvLaunch a) {
   if (K > 0 && ci_hi > ci_lo) {
     const int nchunk = (ci_hi - ci_lo + BKT - 1) / BKT;
     gload(ci_lo);
-    // residual / accumulate target, issued after the first chunk's loads so
-    // the first staging does not wait for them; added in the epilogue
-    if (RES && a.ksplit <= 1 && wk == 0) {
-#pragma unroll
-      for (int m = 0; m < TM; ++m)
-#pragma unroll
-        for (int n = 0; n < TN; ++n) {
-          const int i = min(i0 + wn * WN + n * 32 + l32, G.n_out - 1);
-          const long long t = (long long)i * G.out_step + G.out_off;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int co = min(co0 + wm * WM + m * 32 + (r & 3) + 4 * half + 8 * (r >> 2), a.C_out - 1);
-            float v = 0.f;
-            if (rb) v = rb[co * a.rc + t];
-            if (fold_out) v = v + ob[co * a.oc + t];
-            radd[m][n][r] = v;
-          }
-        }
-    }
     lstore(ci_lo);
     __syncthreads();
     for (int c = 0; c < nchunk; ++c) {
@@ -355,9 +328,7 @@ void conv1d_mfma_kernel(ConvLaunch a) {
         const int row = (r & 3) + 4 * half + 8 * (r >> 2);
         const int co = co0 + wm * WM + m * 32 + row;
         if (co >= a.C_out) continue;
-        float v = acc[m][n][r];
-        if constexpr (RES) v = v + radd[m][n][r];
-        v = apply_act(v, a.out_act, a.out_slope);
+        float v = apply_act(acc[m][n][r], a.out_act, a.out_slope);
         float* o = ob + co * a.oc + t;
         if (G.combine == COMB_ADD && !fold_out) {
           v = *o + v;
@@ -412,15 +383,7 @@ bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
   if (lds > kLdsLimit) return false;
   dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B * std::max(a.ksplit, 1));
   for (int g = 0; g < a.n_groups; ++g) RVC_CHECK(a.g[g].K <= KMAX, "conv1d_mfma: taps exceed the configuration");
-  // launches with a residual or an accumulate target (folded into the result
-  // in the epilogue) take the instantiation that prefetches them
-  bool res = false;
-  for (int g = 0; g < a.n_groups; ++g)
-    res |= a.g[g].res != nullptr || (a.g[g].combine == COMB_ADD && a.out_act == ACT_NONE);
-  if (res && a.ksplit <= 1)
-    hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX, true>), grid, dim3(C::NT), lds, s, a);
-  else
-    hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX, false>), grid, dim3(C::NT), lds, s, a);
+  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX>), grid, dim3(C::NT), lds, s, a);
   check_launch("conv1d_mfma");
   if (a.ksplit > 1) launch_splitk_reduce(a, s);
   return true;
@@ -540,9 +503,14 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
     if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want) ok = launch_cfg<64, 128, 32, 64, 32, 1, 1, 1>(a, s);
     if (ok) return;
   }
-  if (a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
+  // Large grids (decoder stages 1-3): 8-wave 64x256 / 32x512 tiles of 32x64
+  // wave tiles, which keep the registers near 90 per lane, so five waves per
+  // SIMD hide the staging and barrier phases of one another.
+  if (a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 900) ok = launch_cfg<64, 256, 32, 64, 8, 1>(a, s);
+  if (!ok && a.C_out <= 32 && n_blocks(a, 32, 512) >= 900) ok = launch_cfg<32, 512, 32, 64, 8, 1>(a, s);
+  if (!ok && a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)
-    ok = launch_cfg<64, 128, 32, 64, 16, 1>(a, s) || launch_cfg<64, 128, 32, 64, 8, 1>(a, s);
+    ok = launch_cfg<64, 128, 32, 64, 8, 1>(a, s) || launch_cfg<64, 128, 32, 64, 16, 1>(a, s);
   if (!ok && a.C_out <= 32 && n_blocks(a, 32, 256) >= want)
     ok = launch_cfg<32, 256, 32, 64, 16, 1>(a, s) || launch_cfg<32, 256, 32, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 64) >= want)
