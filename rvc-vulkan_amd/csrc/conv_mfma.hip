@@ -14,7 +14,9 @@
 // the masks applied when the registers are stored to LDS, so no wait for
 // those loads sits in front of the MFMAs.  Inside a chunk the LDS operands of
 // step s+1 are read before the MFMAs of step s are issued (two register sets,
-// ordered with sched_group_barrier).
+// ordered with sched_group_barrier).  The large decoder tiles keep two
+// staging buffers: the prefetched registers go into the idle buffer right
+// behind the current chunk's MFMAs, leaving one barrier per chunk.
 //
 // Each wave computes a WM x WN sub-tile with (WM/32)*(WN/32) 32x32
 // accumulators.  With SK > 1 the SK waves that share a sub-tile split the
@@ -38,6 +40,9 @@
 // (grid z = group x batch): the three ResBlocks of a decoder stage, or all
 // ConvTranspose phases, run as one grid.
 #include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
 
 #include "internal.h"
 
@@ -60,7 +65,7 @@ __device__ __forceinline__ float apply_act(float v, int act, float slope) {
 // KMAX: most taps of any group of the launch; it sizes the register
 // prefetch of the weights (1 for the plain GEMMs of 1x1 convolutions, which
 // then afford wide channel chunks).
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1, int KMAX = kConvTapsMax>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1, int KMAX = kConvTapsMax, int NBUF = 1>
 struct Cfg {
   static constexpr int NWM = BM / WM;
   static constexpr int NWN = BN / WN;
@@ -75,7 +80,7 @@ struct Cfg {
   static constexpr int WPT = (KMAX * BKT * W4ROW + NT - 1) / NT;
   static size_t lds_bytes(int K, int dil) {
     const int XW = BN * S + (K > 0 ? (K - 1) * dil : 0);
-    const size_t stage = sizeof(float) * ((size_t)BKT * XW + (size_t)K * BKT * BM);
+    const size_t stage = NBUF * sizeof(float) * ((size_t)BKT * XW + (size_t)K * BKT * BM);
     const size_t red = SK > 1 ? sizeof(float) * (size_t)(SK - 1) * NWM * NWN * TM * TN * 16 * 64 : 0;
     return stage > red ? stage : red;
   }
@@ -85,11 +90,11 @@ struct Cfg {
 // without the cap the compiler spends registers on the accumulator-start
 // loads and drops the 128 x 128 tile to one wave per SIMD (measured 30 %
 // slower).
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S, int KMAX, int NBUF>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * SK * 64)
 __attribute__((amdgpu_waves_per_eu(KMAX == 1 ? 1 : 2)))
 void conv1d_mfma_kernel(ConvLaunch a) {
-  using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX>;
+  using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX, NBUF>;
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = C::BKT;
   constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
   static_assert(BK % 2 == 0 && BKT % 4 == 0, "channel chunk must be a multiple of 4");
@@ -98,20 +103,39 @@ void conv1d_mfma_kernel(ConvLaunch a) {
   const int gi = (blockIdx.z / a.B) % a.n_groups;
   const int ks = blockIdx.z / (a.B * a.n_groups);  // channel split of a split-K launch
   const ConvGroup G = a.g[gi];                      // one set of scalar loads
-  const int i0 = blockIdx.x * BN;
+  // Tile order: workgroups are dispatched x-fastest and dealt round-robin to
+  // the 8 XCDs (each with its own L2).  The C_out tiles of one column tile
+  // read the same input window, so they are mapped 8 dispatch slots apart --
+  // onto the same XCD, close in time -- and the input comes from L2 once.
+  int tx = blockIdx.x, ty = blockIdx.y;
+  if (gridDim.y > 1) {
+    const int nty = gridDim.y;
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int full = (gridDim.x / 8) * 8 * nty;  // linear slots of whole 8-column groups
+    if (lin < full) {
+      tx = (lin / (8 * nty)) * 8 + lin % 8;
+      ty = (lin / 8) % nty;
+    } else {
+      tx = (gridDim.x / 8) * 8 + (lin - full) / nty;
+      ty = (lin - full) % nty;
+    }
+  }
+  const int i0 = tx * BN;
   // input channels of this workgroup: all, or one split of a.ksplit
   const int csplit = a.ksplit > 1 ? a.csplit : a.C_in;
   const int ci_lo = ks * csplit;
   const int ci_hi = min(a.C_in, ci_lo + csplit);
   if (i0 >= G.n_out) return;  // uniform for the whole workgroup, before any barrier
-  const int co0 = blockIdx.y * BM;
+  const int co0 = ty * BM;
   const int K = G.K;
   const int dil = G.dil;
   const int XW = BN * S + (K > 0 ? (K - 1) * dil : 0);
 
+  // NBUF staging buffers of [BKT][XW] inputs then [K][BKT][BM] weights
+  // (BKT*XW and K*BKT*BM are multiples of 4, so every weight block is
+  // 16-byte aligned)
   extern __shared__ float smem[];
-  float* xs = smem;             // [BKT][XW]
-  float* ws = smem + BKT * XW;  // [K][BKT][BM]   (BKT*XW is a multiple of 4)
+  const int stage_floats = BKT * XW + K * BKT * BM;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -201,7 +225,9 @@ void conv1d_mfma_kernel(ConvLaunch a) {
 #pragma unroll
     for (int e = 0; e < WPT; ++e) wreg[e] = *reinterpret_cast<const float4*>(wc0 + (wr_[e] < lim ? wo[e] : 0));
   };
-  auto lstore = [&](int ci0) {
+  auto lstore = [&](int ci0, int buf) {
+    float* xs = smem + buf * stage_floats;
+    float* ws = xs + BKT * XW;
     const int lim = ci_hi - ci0;
 #pragma unroll
     for (int e = 0; e < XPT; ++e) {
@@ -222,12 +248,15 @@ void conv1d_mfma_kernel(ConvLaunch a) {
   if (K > 0 && ci_hi > ci_lo) {
     const int nchunk = (ci_hi - ci_lo + BKT - 1) / BKT;
     gload(ci_lo);
-    lstore(ci_lo);
+    lstore(ci_lo, 0);
     __syncthreads();
     for (int c = 0; c < nchunk; ++c) {
       const bool more = c + 1 < nchunk;
       const int cn = ci_lo + (c + 1) * BKT;
       if (more) gload(cn);
+      const int buf = NBUF > 1 ? (c & 1) : 0;
+      const float* xs = smem + buf * stage_floats;
+      const float* ws = xs + BKT * XW;
       // software-pipelined: the LDS operands of step s+1 are read before the
       // MFMAs of step s are issued (two register sets, chosen by step parity)
       const float* wbase = ws + (wk * BK + half) * BM + wm * WM + l32;
@@ -261,10 +290,18 @@ void conv1d_mfma_kernel(ConvLaunch a) {
           __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
         }
       }
-      __syncthreads();
-      if (more) {
-        lstore(cn);
+      if constexpr (NBUF > 1) {
+        // the other buffer was last read in chunk c - 1, which every wave
+        // finished before the previous barrier: store into it right behind
+        // this chunk's MFMAs, one barrier per chunk
+        if (more) lstore(cn, buf ^ 1);
         __syncthreads();
+      } else {
+        __syncthreads();
+        if (more) {
+          lstore(cn, 0);
+          __syncthreads();
+        }
       }
     }
   }
@@ -341,6 +378,276 @@ void conv1d_mfma_kernel(ConvLaunch a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent variant for the large decoder launches (stride 1, one channel
+// split, STORE with an optional residual or ADD without one).  The grid is one
+// workgroup per resident slot; work item j = (group, batch item, column tile,
+// C_out tile) -- groups in launch order, which the decoder sets heaviest (most
+// taps) first -- goes to workgroup j % gridDim.x, so every workgroup gets the
+// same mix and the short items fill the end.  The (item, chunk) sequence of a
+// workgroup is one software pipeline over two LDS buffers: the next item's
+// first chunk is loaded behind the current item's last chunk, and the
+// current item's residual (or, for ADD, the current output) is prefetched
+// into registers during that last chunk, so neither the start of an item nor
+// its epilogue waits on global memory.  The sum is (conv + bias) + residual,
+// the reference's order, and depends only on the tile shape, never on which
+// workgroup runs the item.
+__device__ __forceinline__ void persist_tile(int lin, int n_tx, int n_ty, int& tx, int& ty) {
+  // the one-shot kernel's XCD-aware order (C_out tiles of one column tile 8
+  // items apart); with a grid that is a multiple of 8, item j runs on XCD j % 8
+  if (n_ty > 1) {
+    const int full = (n_tx / 8) * 8 * n_ty;
+    if (lin < full) {
+      tx = (lin / (8 * n_ty)) * 8 + lin % 8;
+      ty = (lin / 8) % n_ty;
+    } else {
+      tx = (n_tx / 8) * 8 + (lin - full) / n_ty;
+      ty = (lin - full) % n_ty;
+    }
+  } else {
+    tx = lin;
+    ty = 0;
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int BK>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
+__attribute__((amdgpu_waves_per_eu(4)))
+void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floats) {
+  using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
+  constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = BK;
+  constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
+  static_assert(BK % 4 == 0 && (BK / 2) % 2 == 0, "channel chunk must be a multiple of 4");
+
+  const int per_b = n_tx * n_ty;
+  const int per_group = a.B * per_b;
+  const int n_items = per_group * a.n_groups;
+  int item = blockIdx.x;
+  if (item >= n_items) return;  // uniform for the whole workgroup, before any barrier
+  const int nchunk = a.C_in / BKT;  // the launcher requires C_in % BK == 0
+
+  extern __shared__ float smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % C::NWM;
+  const int wn = wave / C::NWM;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+
+  // ---- staging side: the item whose chunks are being loaded.  Loads go
+  // through buffer resources whose range is the chunk's part of the tensor:
+  // padding and masked lanes carry an offset past that range and read 0. ----
+  int s_gi = 0, s_b = 0, s_i0 = 0, s_co0 = 0, s_K = 1, s_dil = 1, s_XW = BN;
+  const float* s_x = nullptr;
+  const float* s_w = nullptr;
+  unsigned xo[XPT], wo[WPT];  // byte offsets from the chunk's first channel
+  constexpr unsigned kOut = 0x80000000u;
+  auto setup = [&](int j) {
+    s_gi = j / per_group;
+    const int r = j - s_gi * per_group;
+    s_b = r / per_b;
+    int tx, ty;
+    persist_tile(r - s_b * per_b, n_tx, n_ty, tx, ty);
+    s_i0 = tx * BN;
+    s_co0 = ty * BM;
+    const ConvGroup& G = a.g[s_gi];
+    s_K = G.K;
+    s_dil = G.dil;
+    s_XW = BN + (s_K - 1) * s_dil;
+    s_x = G.x + (long long)s_b * a.xb;
+    s_w = G.w;
+    const int nx = BKT * s_XW;
+    const int nw4 = s_K * BKT * W4ROW;
+    const int tbase = s_i0 + G.in_off;
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) {
+      const int idx = tid + e * NT;
+      const int row = idx / s_XW;
+      const int t = tbase + idx - row * s_XW;
+      xo[e] = idx < nx && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
+    }
+#pragma unroll
+    for (int e = 0; e < WPT; ++e) {
+      const int idx = tid + e * NT;
+      const int row = idx / W4ROW;
+      const int c4 = idx - row * W4ROW;
+      const int k = row / BKT;
+      const int rr = row - k * BKT;
+      wo[e] = idx < nw4 && s_co0 + 4 * c4 < a.w_ld ? 4u * (unsigned)((k * a.C_in + rr) * a.w_ld + s_co0 + 4 * c4)
+                                                    : kOut;
+    }
+  };
+  float xv[XPT];
+  float4 wreg[WPT];
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  auto gload = [&](int ci0) {
+    // ranges: rows ci0.. of x ((C_in - ci0 - 1) full rows + one of L_in), and
+    // the weight rows k * C_in + ci0 + rr of every tap
+    const unsigned xr = 4u * (unsigned)((a.C_in - ci0 - 1) * (int)a.xc + a.L_in);
+    const unsigned wr = 4u * (unsigned)(((s_K - 1) * a.C_in + a.C_in - ci0) * a.w_ld);
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(s_x + (long long)ci0 * a.xc), (short)0, (int)xr, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(s_w + (long long)ci0 * a.w_ld), (short)0, (int)wr, 0x00020000);
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) xv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xo[e], 0, 0));
+#pragma unroll
+    for (int e = 0; e < WPT; ++e)
+      wreg[e] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wo[e], 0, 0));
+  };
+  auto lstore = [&](int buf) {
+    float* xs = smem + buf * stage_floats;
+    float* ws = xs + BKT * s_XW;
+    const int nx = BKT * s_XW;
+    const int nw4 = s_K * BKT * W4ROW;
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) {
+      const int idx = tid + e * NT;
+      if (idx < nx) {
+        float v = xv[e];
+        if (a.in_act == ACT_LEAKY) v = v >= 0.f ? v : v * a.in_slope;
+        xs[idx] = v;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < WPT; ++e) {
+      const int idx = tid + e * NT;
+      if (idx < nw4) reinterpret_cast<float4*>(ws)[idx] = wreg[e];
+    }
+  };
+
+  // MFMAs of one staged chunk (software-pipelined LDS operands, as in the
+  // one-shot kernel)
+  floatx16 acc[TM][TN];
+  auto mfma_chunk = [&](int buf, int K, int dil, int XW) {
+    const float* xs = smem + buf * stage_floats;
+    const float* ws = xs + BKT * XW;
+    const float* wbase = ws + half * BM + wm * WM + l32;
+    const float* xbase = xs + half * XW + wn * WN + l32;
+    float av[2][TM], bv[2][TN];
+    auto lda = [&](int k, int q, int p) {
+      const float* w_ = wbase + (k * BKT + 2 * q) * BM;
+      const float* x_ = xbase + 2 * q * XW + k * dil;
+#pragma unroll
+      for (int m = 0; m < TM; ++m) av[p][m] = w_[m * 32];
+#pragma unroll
+      for (int n = 0; n < TN; ++n) bv[p][n] = x_[n * 32];
+    };
+    lda(0, 0, 0);
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+      for (int q = 0; q < BK / 2; ++q) {
+        const int p = q & 1;
+        if (q + 1 < BK / 2)
+          lda(k, q + 1, p ^ 1);
+        else
+          lda(k + 1 < K ? k + 1 : k, 0, p ^ 1);
+#pragma unroll
+        for (int m = 0; m < TM; ++m)
+#pragma unroll
+          for (int n = 0; n < TN; ++n)
+            acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[p][m], bv[p][n], acc[m][n], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (TM + 1) / 2 + (TN + 1) / 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+      }
+    }
+  };
+
+  setup(item);
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  int buf = 0;
+  for (; item < n_items; item += gridDim.x) {
+    // the current item's geometry, kept before setup() moves on to the next
+    const int c_gi = s_gi, c_b = s_b, c_i0 = s_i0, c_co0 = s_co0, c_K = s_K, c_dil = s_dil, c_XW = s_XW;
+#pragma unroll
+    for (int m = 0; m < TM; ++m)
+#pragma unroll
+      for (int n = 0; n < TN; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.f;
+    // every chunk but the last: prefetch the next chunk of this item.  The
+    // other buffer was last read in the previous chunk, which every wave
+    // finished before the previous barrier.
+    for (int c = 0; c + 1 < nchunk; ++c) {
+      gload((c + 1) * BKT);
+      mfma_chunk(buf, c_K, c_dil, c_XW);
+      lstore(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+    // the last chunk: prefetch the next item's first chunk and this item's
+    // epilogue operand (the residual, or the current output for ADD)
+    const bool more = item + (int)gridDim.x < n_items;
+    if (more) {
+      setup(item + gridDim.x);
+      gload(0);
+    }
+    // Epilogue addressing through buffer resources over this batch item's
+    // output / residual: lane offset (co_l, t) per column, the row within the
+    // lane's 16 accumulator rows as a uniform offset; columns past n_out get
+    // an out-of-range offset, so their loads read 0 and their stores drop.
+    const ConvGroup& G = a.g[c_gi];
+    const bool res = G.res != nullptr;
+    const bool add = G.combine == COMB_ADD;
+    const int co_l = c_co0 + wm * WM + 4 * half;
+    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(G.out + (long long)c_b * a.ob), (short)0, (int)(4u * (unsigned)(a.C_out * (int)a.oc)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t prs =
+        res ? __builtin_amdgcn_make_buffer_rsrc((void*)(G.res + (long long)c_b * a.rb), (short)0,
+                                                (int)(4u * (unsigned)(a.C_out * (int)a.rc)), 0x00020000)
+            : ors;
+    const int pc = res ? (int)a.rc : (int)a.oc;
+    unsigned ooff[TN], poff[TN];
+#pragma unroll
+    for (int n = 0; n < TN; ++n) {
+      const int i = c_i0 + wn * WN + n * 32 + l32;
+      const int t = i * G.out_step + G.out_off;
+      const bool ok = i < G.n_out;
+      ooff[n] = ok ? 4u * (unsigned)(co_l * (int)a.oc + t) : kOut;
+      poff[n] = ok ? 4u * (unsigned)(co_l * pc + t) : kOut;
+    }
+    float pre[TM][TN][16];
+    if (res || add) {
+#pragma unroll
+      for (int m = 0; m < TM; ++m)
+#pragma unroll
+        for (int n = 0; n < TN; ++n)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int roff = m * 32 + (r & 3) + 8 * (r >> 2);
+            pre[m][n][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, poff[n], 4 * roff * pc, 0));
+          }
+    }
+    mfma_chunk(buf, c_K, c_dil, c_XW);
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+
+    // ---- epilogue: ((acc + bias) [+ res]) -> act -> [pre +] -> store ----
+#pragma unroll
+    for (int m = 0; m < TM; ++m) {
+      float bias[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) bias[r] = G.bias ? G.bias[co_l + m * 32 + (r & 3) + 8 * (r >> 2)] : 0.f;
+#pragma unroll
+      for (int n = 0; n < TN; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int roff = m * 32 + (r & 3) + 8 * (r >> 2);
+          float v = acc[m][n][r];
+          if (G.bias) v = v + bias[r];
+          if (res) v = v + pre[m][n][r];
+          v = apply_act(v, a.out_act, a.out_slope);
+          if (add) v = pre[m][n][r] + v;
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), ors, ooff[n], 4 * roff * (int)a.oc, 0);
+        }
+    }
+  }
+}
+
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
 // added in index order (deterministic), one thread per output element.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(ConvLaunch a) {
@@ -375,17 +682,93 @@ int max_n_out(const ConvLaunch& a) {
   return n;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1, int KMAX = kConvTapsMax>
+template <int BM, int BN, int WM, int WN, int BK, int SK, int S = 1, int KMAX = kConvTapsMax, int NBUF = 1>
 bool launch_cfg(const ConvLaunch& a, hipStream_t s) {
-  using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX>;
+  using C = Cfg<BM, BN, WM, WN, BK, SK, S, KMAX, NBUF>;
   size_t lds = 0;
   for (int g = 0; g < a.n_groups; ++g) lds = std::max(lds, C::lds_bytes(a.g[g].K, a.g[g].dil));
   if (lds > kLdsLimit) return false;
   dim3 grid((max_n_out(a) + BN - 1) / BN, (a.C_out + BM - 1) / BM, a.n_groups * a.B * std::max(a.ksplit, 1));
   for (int g = 0; g < a.n_groups; ++g) RVC_CHECK(a.g[g].K <= KMAX, "conv1d_mfma: taps exceed the configuration");
-  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX>), grid, dim3(C::NT), lds, s, a);
+  hipLaunchKernelGGL((conv1d_mfma_kernel<BM, BN, WM, WN, BK, SK, S, KMAX, NBUF>), grid, dim3(C::NT), lds, s, a);
   check_launch("conv1d_mfma");
   if (a.ksplit > 1) launch_splitk_reduce(a, s);
+  return true;
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static std::atomic<int> cache[16];
+  int dev = 0;
+  RVC_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 16) {
+    int n = 0;
+    RVC_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    return n;
+  }
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    RVC_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Workgroups of `kernel` resident per CU with `lds` bytes of dynamic LDS
+// (cached per kernel and LDS size: the decoder issues the same few shapes).
+int resident_blocks(const void* kernel, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, size_t>, int> cache;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find({kernel, lds});
+  if (it != cache.end()) return it->second;
+  int nb = 0;
+  RVC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, kernel, threads, lds));
+  cache[{kernel, lds}] = nb;
+  return nb;
+}
+
+// The persistent kernel takes stride-1 launches without a channel split, a
+// second bias or ADD_DIV, with whole 8-channel chunks, whose groups either
+// store (optionally adding a residual) or accumulate without a residual.
+bool persist_ok(const ConvLaunch& a) {
+  if (a.bias2 || a.ksplit > 1 || a.C_in % 8 != 0) return false;
+  // 32-bit byte offsets within one batch item's tensors
+  const long long lim = 1LL << 31;
+  if (4LL * a.C_out * a.oc >= lim || 4LL * a.C_out * a.rc >= lim || 4LL * a.C_in * a.xc >= lim) return false;
+  for (int g = 0; g < a.n_groups; ++g) {
+    const ConvGroup& G = a.g[g];
+    if (G.K < 1 || G.in_step > 1) return false;
+    if (G.combine == COMB_ADD_DIV || (G.combine == COMB_ADD && G.res)) return false;
+  }
+  return true;
+}
+
+template <int BM, int BN, int WM, int WN, int BK>
+bool launch_persist(const ConvLaunch& a, hipStream_t s) {
+  using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
+  if (a.C_out % BM != 0) return false;  // the epilogue has no row guard
+  int stage = 0;  // floats per staging buffer: the largest group
+  for (int g = 0; g < a.n_groups; ++g) {
+    const int XW = BN + (a.g[g].K - 1) * a.g[g].dil;
+    stage = std::max(stage, BK * XW + a.g[g].K * BK * BM);
+  }
+  stage = (stage + 3) / 4 * 4;  // keeps each buffer's weight block 16-byte aligned
+  const size_t lds = 2 * sizeof(float) * (size_t)stage;
+  if (lds > kLdsLimit) return false;
+  const int n_tx = (max_n_out(a) + BN - 1) / BN;
+  const int n_ty = (a.C_out + BM - 1) / BM;
+  const long long items = (long long)a.B * n_tx * n_ty * a.n_groups;
+  RVC_CHECK(items < (1LL << 30), "conv1d_mfma: launch too large");
+  const void* kern = reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK>);
+  const int per_cu = resident_blocks(kern, C::NT, lds);
+  if (per_cu < 1) return false;
+  long long grid = (long long)per_cu * device_cus();
+  if (grid >= 8) grid -= grid % 8;  // item j then runs on XCD j % 8
+  grid = std::min(grid, items);
+  hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK>), dim3((unsigned)grid), dim3(C::NT), lds, s, a,
+                     n_tx, n_ty, stage);
+  check_launch("conv1d_mfma_persist");
   return true;
 }
 
@@ -506,8 +889,11 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   // Large grids (decoder stages 1-3): 8-wave 64x256 / 32x512 tiles of 32x64
   // wave tiles, which keep the registers near 90 per lane, so five waves per
   // SIMD hide the staging and barrier phases of one another.
-  if (a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 900) ok = launch_cfg<64, 256, 32, 64, 8, 1>(a, s);
-  if (!ok && a.C_out <= 32 && n_blocks(a, 32, 512) >= 900) ok = launch_cfg<32, 512, 32, 64, 8, 1>(a, s);
+  const bool persist = persist_ok(a);
+  if (a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 900)
+    ok = (persist && launch_persist<64, 256, 32, 64, 8>(a, s)) || launch_cfg<64, 256, 32, 64, 8, 1>(a, s);
+  if (!ok && a.C_out <= 32 && n_blocks(a, 32, 512) >= 900)
+    ok = (persist && launch_persist<32, 512, 32, 64, 8>(a, s)) || launch_cfg<32, 512, 32, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
   if (!ok && a.C_out % 64 == 0 && n_blocks(a, 64, 128) >= want)
     ok = launch_cfg<64, 128, 32, 64, 8, 1>(a, s) || launch_cfg<64, 128, 32, 64, 16, 1>(a, s);
