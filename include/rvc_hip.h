@@ -282,6 +282,51 @@ int32_t rvc_hubert_set_debug(int64_t s, int32_t keep);
 int32_t rvc_hubert_set_timing(int64_t s, const char* tag);
 int32_t rvc_hubert_get_timing(int64_t s, double* total_ms, int64_t* launches, double* flops, double* bytes);
 
+/* ---------------------------------------------------------------- conversion glue session
+ * No counterpart in the reference ABI.  The steps of runtime/pipeline.py either
+ * side of SynthesizerTrn.infer, on device: feature retrieval against a resident
+ * index (search_l2, runtime/retrieval.py:35-83, and the blend of
+ * runtime/pipeline.py:546-566), the 2x feature interpolation and pitch protect
+ * mask (runtime/pipeline.py:568-610, runtime/nn.py:734-758), the RMS envelope
+ * mix (change_rms, runtime/pipeline.py:164-232) and the int16 peak
+ * normalisation (runtime/pipeline.py:1208-1213).  Features are row-major
+ * [F, D] (the HuBERT output layout). */
+int64_t rvc_vc_create(int64_t h);
+int32_t rvc_vc_destroy(int64_t v);
+/* Make vectors [n, dim] the resident retrieval index (FeatureIndex.add +
+ * reconstruct_n, runtime/retrieval.py:113-140); replaces any previous one. */
+int32_t rvc_vc_set_index(int64_t v, const float* vectors, int64_t n, int64_t dim);
+int32_t rvc_vc_index_info(int64_t v, int64_t* n, int64_t* dim);
+/* search_l2 (runtime/retrieval.py:35-83): the k (1..min(8, n)) nearest index
+ * rows of each query row, squared L2 distances ascending (clamped at 0) and
+ * int64 row numbers; equal distances keep the lower row first. */
+int32_t rvc_vc_search(int64_t v, const float* query, int64_t F, int64_t k, float* scores, int64_t* inds);
+int32_t rvc_vc_search_dev(int64_t v, int64_t query, int64_t F, int64_t k, int64_t scores, int64_t inds);
+/* Pipeline._vc_prepare's feature path (runtime/pipeline.py:488-614, FeatureIndex
+ * branch): when index_rate != 0 and an index is set, feats = blend * index_rate
+ * + feats * (1 - index_rate) with blend the (1/d)^2-weighted mean of the 8
+ * nearest index rows; then 2x linear interpolation to [2F, D]; then, when
+ * pitchf [2F] (already aligned to 2F frames) is given, the protect mask
+ * out = feats * pff + feats0 * (1 - pff), pff = 1 where pitchf > 0, protect
+ * where pitchf < 1, feats0 the interpolated features before retrieval.
+ * pitchf null (or buffer 0): no protect mask (protect >= 0.5 in the reference). */
+int32_t rvc_vc_prepare(int64_t v, const float* feats, int64_t F, int64_t D, double index_rate,
+                       const float* pitchf, double protect, float* out);
+int32_t rvc_vc_prepare_dev(int64_t v, int64_t feats, int64_t F, int64_t D, double index_rate, int64_t pitchf,
+                           double protect, int64_t out);
+/* change_rms(data1, data2, sr1, sr2, rate) (runtime/pipeline.py:164-188):
+ * data2 * rms1^(1-rate) * max(rms2, 1e-6)^(rate-1), the half-second frame RMS
+ * curves linearly interpolated to n2 samples. */
+int32_t rvc_vc_change_rms(int64_t v, const float* data1, int64_t n1, int64_t sr1, const float* data2, int64_t n2,
+                          int64_t sr2, double rate, float* out);
+int32_t rvc_vc_change_rms_dev(int64_t v, int64_t data1, int64_t n1, int64_t sr1, int64_t data2, int64_t n2,
+                              int64_t sr2, double rate, int64_t out);
+/* int16(x * 32768 / max(1, max|x| / 0.99)) (runtime/pipeline.py:1208-1213). */
+int32_t rvc_vc_to_int16(int64_t v, const float* x, int64_t n, int16_t* out);
+int32_t rvc_vc_to_int16_dev(int64_t v, int64_t x, int64_t n, int64_t out);
+int32_t rvc_vc_set_timing(int64_t v, const char* tag);
+int32_t rvc_vc_get_timing(int64_t v, double* total_ms, int64_t* launches, double* flops, double* bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -131,6 +131,20 @@ SYMBOLS = {
     "rvc_hubert_set_timing": (I32, [I64, CHARP]),
     "rvc_hubert_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL),
                                     ctypes.POINTER(DBL)]),
+    "rvc_vc_create": (I64, [I64]),
+    "rvc_vc_destroy": (I32, [I64]),
+    "rvc_vc_set_index": (I32, [I64, F32P, I64, I64]),
+    "rvc_vc_index_info": (I32, [I64, I64P, I64P]),
+    "rvc_vc_search": (I32, [I64, F32P, I64, I64, F32P, I64P]),
+    "rvc_vc_search_dev": (I32, [I64, I64, I64, I64, I64, I64]),
+    "rvc_vc_prepare": (I32, [I64, F32P, I64, I64, DBL, F32P, DBL, F32P]),
+    "rvc_vc_prepare_dev": (I32, [I64, I64, I64, I64, DBL, I64, DBL, I64]),
+    "rvc_vc_change_rms": (I32, [I64, F32P, I64, I64, F32P, I64, I64, DBL, F32P]),
+    "rvc_vc_change_rms_dev": (I32, [I64, I64, I64, I64, I64, I64, I64, DBL, I64]),
+    "rvc_vc_to_int16": (I32, [I64, F32P, I64, ctypes.POINTER(ctypes.c_int16)]),
+    "rvc_vc_to_int16_dev": (I32, [I64, I64, I64, I64]),
+    "rvc_vc_set_timing": (I32, [I64, CHARP]),
+    "rvc_vc_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL), ctypes.POINTER(DBL)]),
 }
 
 
