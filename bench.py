@@ -13,9 +13,12 @@ the session stream over the timed steps) and a CPU baseline (the numpy
 oracle on a bounded 1 s sample of the same workload, on this host).
 
 ``--workload hubert`` measures BASELINE config 3 instead (HuBERT-base
-encoder, 10 s of 16 kHz audio -> [1, 499, 768]) and ``--workload dec48k-b8``
-config 4 (48k GeneratorNSF, 8 chunks of 6 s as one batch); each prints its
-own JSON line in the same format.  The default run is config 2.
+encoder, 10 s of 16 kHz audio -> [1, 499, 768]), ``--workload dec48k-b8``
+config 4 (48k GeneratorNSF, 8 chunks of 6 s as one batch), ``--workload
+synth40k-bf16-b4`` config 5, and ``--workload vc40k`` the device-resident
+conversion chain around config 2 (HuBERT, retrieval, synthesis, RMS mix,
+int16); each prints its own JSON line in the same format.  The default run
+is config 2.
 """
 
 from __future__ import annotations
@@ -370,13 +373,122 @@ def bench_bf16(args, precision):
     return 0
 
 
+VC_INDEX_ROWS = 20000  # retrieval index size of the vc40k workload (HuBERT-v2 width 768)
+
+
+def bench_vc(args):
+    """The device-resident conversion chain around config 2 (not a BASELINE
+    config; reported beside it): 10 s of 16 kHz input -> HuBERT-base
+    (config 3) -> retrieval blend against a 20 000-row index at index_rate
+    0.75, 2x interpolation and the protect mask (protect 0.33) -> the 40k
+    synthesizer of config 2 on the 2 x 499 = 998 frames -> change_rms
+    (rate 0.25) -> int16.  Pitch is an input (F0 extraction is outside this
+    backend).  One step = the five device calls on resident buffers."""
+    from rvc_hip import _hip, synthetic as syn
+    from rvc_hip.hip_ops import get_context
+    from rvc_hip.hubert import HipHubert
+    from rvc_hip.pipeline import HipVcGlue
+    from rvc_hip.synth import HipSynthesizer
+
+    if not _hip.has_so:
+        raise RuntimeError(f"HIP backend missing: {_hip.so_load_error}")
+    ctx = get_context()
+    geom = syn.GEOM_40K
+    T = 160000
+    hub = HipHubert(syn.make_hubert_weights(syn.HUBERT_BASE, seed=0), ctx=ctx)
+    s = HipSynthesizer(syn.make_weights(geom, seed=0), sr=geom.sr, ctx=ctx)
+    glue = HipVcGlue(ctx)
+    rng = np.random.default_rng(5)
+    glue.set_index(rng.standard_normal((VC_INDEX_ROWS, 768)).astype(np.float32))
+    _log(f"bench: device {_hip.device_name()}; HuBERT, synthesizer and index resident")
+    L = hub.frames(T)
+    P = 2 * L
+    inp = syn.make_synth_inputs(geom, P, seed=3)
+    x = syn.make_hubert_input(T, seed=3)
+    ids = {
+        "x": ctx.upload(x), "feats": ctx.alloc(L * 768), "phone": ctx.alloc(P * 768),
+        "pitch": ctx.upload(np.ascontiguousarray(inp["pitch"], np.int64)),
+        "f0": ctx.upload(np.ascontiguousarray(inp["nsff0"], np.float32)),
+        "sid": ctx.upload(np.ascontiguousarray(inp["sid"], np.int64)),
+        "nz": ctx.upload(np.ascontiguousarray(inp["nz"], np.float32)),
+        "ns": ctx.upload(np.ascontiguousarray(inp["ns"], np.float32).reshape(-1)),
+    }
+    n_out = P * geom.upp
+    ids["wave"] = ctx.alloc(n_out)
+    ids["mix"] = ctx.alloc(n_out)
+    ids["i16"] = ctx.alloc((n_out + 1) // 2)
+    stages = {
+        "hubert": lambda: hub.encode_dev(ids["x"], 1, T, ids["feats"], version=2),
+        "prepare": lambda: glue.prepare_dev(ids["feats"], L, 768, 0.75, ids["f0"], 0.33, ids["phone"]),
+        "synth": lambda: s.infer_dev(ids["phone"], ids["pitch"], ids["f0"], ids["sid"], ids["nz"], ids["ns"], 1, P,
+                                     ids["wave"]),
+        "change_rms": lambda: glue.change_rms_dev(ids["x"], T, 16000, ids["wave"], n_out, geom.sr, 0.25, ids["mix"]),
+        "int16": lambda: _hip._check(_hip.get_lib().rvc_vc_to_int16_dev(glue.handle, ids["mix"], n_out, ids["i16"]),
+                                     "rvc_vc_to_int16_dev"),
+    }
+
+    def step():
+        for fn in stages.values():
+            fn()
+
+    for _ in range(args.warmup):
+        step()
+    s.set_timing("dec.rb")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = time.perf_counter() - t0
+    rb = s.get_timing()
+    s.set_timing("")
+    audio_s = T / 16000.0
+    value = audio_s * args.steps / dt
+    _log(f"bench vc40k: {dt * 1e3 / args.steps:.3f} ms/step, {value:.1f} audio-s/s")
+    n = max(rb["launches"], 1)
+    avg_s = rb["ms"] / 1e3 / n
+    achieved = rb["flops"] / n / avg_s / 1e12 if avg_s > 0 else 0.0
+    roofline = {"kernel": "conv1d_mfma (GeneratorNSF ResBlock convs, all stages)", "bound": "mfma",
+                "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n // args.steps,
+                "share_of_step": round(rb["ms"] / (dt * 1e3), 3)}
+    breakdown = {}
+    if not args.quick:
+        reps = 5
+        for name, fn in stages.items():
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            breakdown[name] = {"ms": round((time.perf_counter() - t0) * 1e3 / reps, 4)}
+        for tag in ("vc.knn.gemm", "vc.knn.select", "vc.blend", "vc.interp", "vc.rms", "vc.int16"):
+            glue.set_timing(tag)
+            stages["prepare"]()
+            stages["change_rms"]()
+            stages["int16"]()
+            breakdown[tag] = family_entry(glue.get_timing())
+        glue.set_timing("")
+    line = {
+        "metric": "audio-sec converted/sec (HuBERT + retrieval + 40k synthesis + RMS mix, 10 s @16 kHz in, 1 GPU)",
+        "value": round(value, 2), "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded input, random-init weights and index)",
+        "config": {"workload": f"vc40k: 160000 samples @16 kHz -> HuBERT-base [1,{L},768] -> retrieval over "
+                               f"{VC_INDEX_ROWS} rows (index_rate 0.75) + 2x interpolation + protect 0.33 -> "
+                               f"40k synthesis P={P} -> change_rms 0.25 -> int16",
+                   "samples_in": T, "frames": P, "batch": 1, "index_rows": VC_INDEX_ROWS, "output_samples": n_out},
+        "roofline": roofline, "cpu_baseline": None, "breakdown": breakdown,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", default="synth40k",
-                    choices=("synth40k", "hubert", "dec48k-b8", "synth40k-bf16-b4", "synth40k-bf16rb-b4"),
+                    choices=("synth40k", "hubert", "dec48k-b8", "synth40k-bf16-b4", "synth40k-bf16rb-b4", "vc40k"),
                     help="synth40k: BASELINE config 2 (default); hubert: config 3; dec48k-b8: config 4; "
                          "synth40k-bf16-b4: config 5 (ups + enc_p matmuls on bf16); synth40k-bf16rb-b4: config 5 "
-                         "with the ResBlocks on bf16 too (reported separately)")
+                         "with the ResBlocks on bf16 too (reported separately); vc40k: the conversion chain "
+                         "HuBERT -> retrieval -> synthesis -> RMS mix -> int16 around config 2")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -398,6 +510,8 @@ def main():
         return bench_hubert(args)
     if args.workload == "dec48k-b8":
         return bench_dec48(args)
+    if args.workload == "vc40k":
+        return bench_vc(args)
     if args.workload.startswith("synth40k-bf16"):
         return bench_bf16(args, precision=1 if args.workload == "synth40k-bf16-b4" else 2)
 

@@ -35,14 +35,15 @@ __global__ __launch_bounds__(256) void row_sqnorm_kernel(const float* x, float* 
   if (lane == 0) out[r] = s;
 }
 
-// Keep the kTopK smallest (distance, row) pairs, ascending; a candidate
-// displaces an entry only when strictly smaller, so among equal distances the
-// one seen first (the lower row, as rows are visited in order) stays first.
+// Keep the kTopK smallest (distance, row) pairs in lexicographic order:
+// among equal distances the lower row ranks first, whatever order the
+// candidates arrive in (a NaN distance compares false and is never kept).
+__device__ __forceinline__ bool lex_less(float d, int n, float bd, int bn) { return d < bd || (d == bd && n < bn); }
 __device__ __forceinline__ void topk_insert(float (&bs)[kTopK], int (&bi)[kTopK], float d, int n) {
-  if (!(d < bs[kTopK - 1])) return;
+  if (!lex_less(d, n, bs[kTopK - 1], bi[kTopK - 1])) return;
 #pragma unroll
   for (int j = 0; j < kTopK; ++j) {
-    const bool sw = d < bs[j];
+    const bool sw = lex_less(d, n, bs[j], bi[j]);
     const float tb = bs[j];
     const int ti = bi[j];
     bs[j] = sw ? d : tb;
@@ -71,11 +72,23 @@ __global__ __launch_bounds__(64) void knn_partial_kernel(const float* dot, long 
   }
   if (f < F) {
     const float qq = q2[f];
-    for (int n = n0; n < n1; ++n) {
-      float d = (qq + d2[n]) - 2.0f * dot[(long long)n * ldd + f];
-      d = d < 0.f ? 0.f : d;  // np.maximum(dist, 0): a NaN stays NaN and is never kept
-      topk_insert(bs, bi, d, n);
+    auto dist = [&](float dd, float v) {
+      const float d = (qq + dd) - 2.0f * v;
+      return d < 0.f ? 0.f : d;  // np.maximum(dist, 0): a NaN stays NaN and is never kept
+    };
+    // blocks of 16 rows: the 16 loads are issued before any is consumed
+    int n = n0;
+    for (; n + 16 <= n1; n += 16) {
+      float v[16], dd[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        v[u] = dot[(long long)(n + u) * ldd + f];
+        dd[u] = d2[n + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) topk_insert(bs, bi, dist(dd[u], v[u]), n + u);
     }
+    for (; n < n1; ++n) topk_insert(bs, bi, dist(d2[n], dot[(long long)n * ldd + f]), n);
     const long long o = ((long long)s * F + f) * kTopK;
 #pragma unroll
     for (int j = 0; j < kTopK; ++j) {
@@ -85,13 +98,15 @@ __global__ __launch_bounds__(64) void knn_partial_kernel(const float* dot, long 
   }
 }
 
-// Merge the slices' partial lists of each query (slice order = row order, so
-// the strict comparison keeps the lower row among equal distances) and write
-// the first k as scores [F][k] / indices [F][k] (int64).
+// Merge the slices' partial lists of each query, one wave per query: lane l
+// folds slices l, l+64, ... into its own list, then a butterfly over the
+// wave merges the 64 lists (every lane ends with the full top list); the
+// first k entries go to scores [F][k] / indices [F][k] (int64).
 __global__ __launch_bounds__(256) void knn_merge_kernel(const float* ps, const int* pi, int F, int S, int k,
                                                         float* scores, long long* inds) {
-  const int f = blockIdx.x * 256 + threadIdx.x;
-  if (f >= F) return;
+  const int f = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (f >= F) return;  // whole waves
   float bs[kTopK];
   int bi[kTopK];
 #pragma unroll
@@ -99,17 +114,39 @@ __global__ __launch_bounds__(256) void knn_merge_kernel(const float* ps, const i
     bs[j] = INFINITY;
     bi[j] = INT_MAX;
   }
-  for (int s = 0; s < S; ++s) {
+  for (int s = lane; s < S; s += 64) {
     const long long o = ((long long)s * F + f) * kTopK;
+    float cs[kTopK];
+    int ci[kTopK];
 #pragma unroll
-    for (int j = 0; j < kTopK; ++j) topk_insert(bs, bi, ps[o + j], pi[o + j]);
+    for (int j = 0; j < kTopK; ++j) {
+      cs[j] = ps[o + j];
+      ci[j] = pi[o + j];
+    }
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j) topk_insert(bs, bi, cs[j], ci[j]);
   }
 #pragma unroll
-  for (int j = 0; j < kTopK; ++j)
-    if (j < k) {
-      scores[(long long)f * k + j] = bs[j];
-      inds[(long long)f * k + j] = bi[j] == INT_MAX ? -1 : bi[j];
+  for (int off = 32; off >= 1; off >>= 1) {
+    float os[kTopK];
+    int oi[kTopK];
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j) {
+      os[j] = __shfl_xor(bs[j], off);
+      oi[j] = __shfl_xor(bi[j], off);
     }
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j) topk_insert(bs, bi, os[j], oi[j]);
+  }
+  if (lane < k) {
+    // lane j writes entry j (registers indexed by a compile-time j)
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j)
+      if (j == lane) {
+        scores[(long long)f * k + j] = bs[j];
+        inds[(long long)f * k + j] = bi[j] == INT_MAX ? -1 : bi[j];
+      }
+  }
 }
 
 // Retrieval blend of runtime/pipeline.py:546-566 (FeatureIndex branch, brute
@@ -290,9 +327,11 @@ void launch_row_sqnorm(const float* x, float* out, long long rows, int cols, hip
 }
 
 int knn_slices(int N) {
-  // about 2 000 database rows per slice, at most 64 slices
-  int S = (N + 1999) / 2000;
-  return S < 1 ? 1 : (S > 64 ? 64 : S);
+  // about 128 index rows per wave (a lane scans them one by one), at most
+  // 256 slices, so F / 64 x slices waves fill the GPU for the usual few
+  // hundred query frames; the merge reads slices x 8 candidates per query
+  int S = (N + 127) / 128;
+  return S < 1 ? 1 : (S > 256 ? 256 : S);
 }
 
 void launch_knn(const float* dot, long long ldd, const float* q2, const float* d2, int F, int N, int k,
@@ -304,7 +343,7 @@ void launch_knn(const float* dot, long long ldd, const float* q2, const float* d
   hipLaunchKernelGGL(knn_partial_kernel, dim3(blocks_for(F, 64), S), dim3(64), 0, s, dot, ldd, q2, d2, F, N, per,
                      part_s, part_i);
   check_launch("knn_partial");
-  hipLaunchKernelGGL(knn_merge_kernel, dim3(blocks_for(F, 256)), dim3(256), 0, s, part_s, part_i, F, S, k, scores,
+  hipLaunchKernelGGL(knn_merge_kernel, dim3(blocks_for(F, 4)), dim3(256), 0, s, part_s, part_i, F, S, k, scores,
                      inds);
   check_launch("knn_merge");
 }
