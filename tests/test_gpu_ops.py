@@ -70,6 +70,21 @@ def test_conv1d_resblock_shapes(ops, C, L, k, d):
     assert rel_l2(got, nn.conv1d(x, w, b, padding=pad, dilation=d)) < TOL
 
 
+@pytest.mark.parametrize("C,L,k,d", [(256, 30000, 3, 1), (128, 120000, 3, 3), (64, 240000, 3, 1),
+                                     (32, 500000, 3, 5)])
+def test_conv1d_persistent_tiles(ops, C, L, k, d):
+    """Grids large enough for the persistent MFMA kernel (32 x 256, 64 x 256
+    and 32 x 512 tiles, buffer-resource staging with out-of-range padding)."""
+    print(f"persistent conv C={C} L={L} k={k} d={d}", flush=True)
+    rng = np.random.default_rng(C + L)
+    x = _r(rng, 1, C, L)
+    w = _r(rng, C, C, k, scale=1.0 / np.sqrt(C * k))
+    b = _r(rng, C, scale=0.1)
+    pad = (k * d - d) // 2
+    got = ops.conv1d(x, w, b, padding=pad, dilation=d)
+    assert rel_l2(got, nn.conv1d(x, w, b, padding=pad, dilation=d)) < TOL
+
+
 @pytest.mark.parametrize("C_in,C_out,L,K", [(192, 512, 200, 7), (192, 768, 300, 3), (768, 192, 300, 3),
                                             (192, 384, 257, 5), (192, 576, 1000, 1)])
 def test_conv1d_encoder_flow_shapes(ops, C_in, C_out, L, K):

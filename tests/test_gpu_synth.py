@@ -126,6 +126,19 @@ def test_config1_decoder_full_size():
     assert np.abs(wave - want).max() <= WAVE_TOL
 
 
+def test_decoder_P400_vs_oracle():
+    """4 s decode (P=400): stages 1-3 run on the persistent MFMA kernel
+    (ResBlock conv1 with leaky input, conv2 with the prefetched residual)."""
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=2)
+    s = _hip_synth(w, sr=geom.sr)
+    inp = syn.make_dec_inputs(geom, 400, seed=12)
+    wave = s.dec_forward(inp["z"], inp["f0"], inp["g"], inp["ns"])
+    want = V.GeneratorNSF(w, V.VitsConfig(w, sr=geom.sr)).forward(inp["z"], inp["f0"], inp["g"], inp["ns"])
+    assert wave.shape == (1, 1, 160000)
+    assert np.abs(wave - want).max() <= WAVE_TOL
+
+
 def test_batch_equals_per_chunk_and_determinism():
     geom = syn.GEOM_48K
     w = syn.make_weights(geom, seed=6)
