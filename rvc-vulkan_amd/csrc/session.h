@@ -148,16 +148,19 @@ struct SessionBase {
     RVC_HIP(hipEventCreate(&e));
     return e;
   }
+  // Run fn (launches on stream st, the engine stream by default); when the
+  // tag is timed, bracket it with events on that stream.
   template <class Fn>
-  void run(const char* t, double flops, double bytes, Fn&& fn) {
+  void run(const char* t, double flops, double bytes, Fn&& fn, hipStream_t st = nullptr) {
     if (!timed(t)) {
       fn();
       return;
     }
+    if (!st) st = eng->stream;
     Ev e{ev(), ev(), flops, bytes};
-    RVC_HIP(hipEventRecord(e.a, eng->stream));
+    RVC_HIP(hipEventRecord(e.a, st));
     fn();
-    RVC_HIP(hipEventRecord(e.b, eng->stream));
+    RVC_HIP(hipEventRecord(e.b, st));
     pending.push_back(e);
   }
   void collect_timing() {

@@ -71,6 +71,24 @@ struct Synth : SessionBase {
   };
   std::vector<StageW> stages;
 
+  // ---- side stream ----
+  // The NSF source, the noise convs and the decoder's cond projection depend
+  // only on f0, the noise and g, so they run on a second (default-priority)
+  // stream while enc_p and flow run on the engine stream; conv_pre waits on
+  // `joined`. Each upsample stage keeps its noise conv output in a buffer of
+  // its own (dN<i>), into which the ConvTranspose then accumulates.
+  hipStream_t side = nullptr;
+  hipEvent_t forked = nullptr, joined = nullptr;
+  float* dec_cv = nullptr;
+  std::vector<float*> dec_noise;
+
+  ~Synth() override {
+    if (side) (void)hipStreamSynchronize(side);
+    if (forked) (void)hipEventDestroy(forked);
+    if (joined) (void)hipEventDestroy(joined);
+    if (side) (void)hipStreamDestroy(side);
+  }
+
   // ---- workspace ----
   bool keep_stages = false;
   std::string z_name = "z_p";  // workspace buffer holding the last flow output
@@ -305,12 +323,15 @@ struct Synth : SessionBase {
   }
 
   // -------------------------------------------------------------- enc_p + flow
-  // Returns the flow output z [B][H][P] (batch stride H*P) and g [B][gin].
-  const float* enc_flow(const float* phone, const long long* pitch, const long long* sid, const float* nz, int B, int P,
-                        float* g) {
+  // g [B][gin] = emb_g(sid)
+  void speaker(const long long* sid, int B, float* g) {
+    launch_gather_rows_i64(sid, emb_g, g, B, n_spk, gin, eng->stream);
+  }
+
+  // Returns the flow output z [B][H][P] (batch stride H*P); g from speaker().
+  const float* enc_flow(const float* phone, const long long* pitch, const float* nz, int B, int P, const float* g) {
     hipStream_t s = eng->stream;
     const long long HP = (long long)H * P;
-    launch_gather_rows_i64(sid, emb_g, g, B, n_spk, gin, s);
     float* phT = buf("phT", (size_t)B * phone_dim * P);
     launch_transpose(phone, phT, B, P, phone_dim, 1.0f, s);
     float* E = buf("encE", (size_t)B * HP);
@@ -382,18 +403,65 @@ struct Synth : SessionBase {
   }
 
   // -------------------------------------------------------------- GeneratorNSF
-  void decode(const float* z, long long zb, const float* g, const float* f0, const float* ns, int B, int P,
-              float* wave) {
-    hipStream_t s = eng->stream;
+  // Side-stream half of the decoder: the harmonic source, each stage's noise
+  // conv (into dN<i>) and cv = cond(g). Ordered after everything already on
+  // the engine stream; decode_main() waits for it.
+  void decode_prep(const float* g, const float* f0, const float* ns, int B, int P) {
+    if (!side) {
+      RVC_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+      RVC_HIP(hipEventCreateWithFlags(&forked, hipEventDisableTiming));
+      RVC_HIP(hipEventCreateWithFlags(&joined, hipEventDisableTiming));
+    }
     const long long N = (long long)P * upp;
     float* har = buf("har", (size_t)B * N);
     float* phase = buf("phase", (size_t)B * P);
+    dec_cv = buf("dec_cond", (size_t)B * U);
+    dec_noise.assign(n_ups, nullptr);
+    {
+      long long L = P;
+      for (int i = 0; i < n_ups; ++i) {
+        L *= rates[i];
+        dec_noise[i] = buf("dN" + std::to_string(i), (size_t)B * chans[i] * L);
+      }
+    }
+    RVC_HIP(hipEventRecord(forked, eng->stream));
+    RVC_HIP(hipStreamWaitEvent(side, forked, 0));
+    hipStream_t s = side;
     run("dec.sine", 20.0 * B * N, 4.0 * B * (2.0 * N + P),
-        [&] { launch_sine_source(f0, ns, har, phase, B, P, upp, (float)sr, w_lin, b_lin, s); });
-    float* cv = buf("dec_cond", (size_t)B * U);
-    launch_gemv(dcond_w, dcond_b, g, gin, cv, U, B, U, gin, s);
+        [&] { launch_sine_source(f0, ns, har, phase, B, P, upp, (float)sr, w_lin, b_lin, s); }, s);
+    launch_gemv(dcond_w, dcond_b, g, gin, dec_cv, U, B, U, gin, s);
+    char tg[32];
+    long long L = P;
+    for (int i = 0; i < n_ups; ++i) {
+      const int C = chans[i];
+      L *= rates[i];
+      const long long CL = (long long)C * L;
+      DirectConvArgs d{};
+      d.x = har; d.xb = N; d.xc = N;
+      d.w = stages[i].nw; d.bias = stages[i].nb;
+      d.out = dec_noise[i]; d.ob = CL; d.oc = L;
+      d.C_in = 1; d.C_out = C; d.L_in = (int)N;
+      d.n_out = (int)((N + 2 * (noise_s[i] / 2) - noise_k[i]) / noise_s[i] + 1);
+      RVC_CHECK(d.n_out == L, "noise conv length does not match the upsampled length");
+      d.K = noise_k[i]; d.stride = noise_s[i]; d.dil = 1; d.in_off = -(noise_s[i] / 2);
+      d.combine = COMB_STORE; d.div = 1.f; d.B = B;
+      std::snprintf(tg, sizeof tg, "dec.noise.s%d", i);
+      run(tg, 2.0 * B * CL * noise_k[i], 4.0 * B * ((double)N + CL), [&] { launch_conv1d_direct(d, s); }, s);
+    }
+    RVC_HIP(hipEventRecord(joined, side));
+  }
+
+  void decode(const float* z, long long zb, const float* g, const float* f0, const float* ns, int B, int P,
+              float* wave) {
+    decode_prep(g, f0, ns, B, P);
+    decode_main(z, zb, B, P, wave);
+  }
+
+  // Engine-stream half: conv_pre (+cv), then per stage ConvTranspose into the
+  // stage's noise buffer, the three ResBlocks and their mean, then conv_post.
+  void decode_main(const float* z, long long zb, int B, int P, float* wave) {
+    hipStream_t s = eng->stream;
     const size_t cap = dec_cap(P);
-    float* X = buf("dX", (size_t)B * cap);
     float* A = buf("dA", (size_t)B * cap);
     float* T[3];
     float* Y[3];
@@ -403,8 +471,9 @@ struct Synth : SessionBase {
     }
     float* pre = buf("dec_pre", (size_t)B * U * P);
     ConvLaunch ca = cargs_same(z, zb, P, dpre_w, dpre_b, pre, (long long)U * P, P, B, H, U, P, 7, 1, 3);
-    ca.bias2 = cv;
+    ca.bias2 = dec_cv;
     ca.bias2b = U;
+    RVC_HIP(hipStreamWaitEvent(s, joined, 0));
     conv("dec.pre", ca);
     const float* cur = pre;
     int L = P, c_in = U;
@@ -415,20 +484,7 @@ struct Synth : SessionBase {
       const int C = chans[i];
       const int Lo = L * rates[i];
       const long long CL = (long long)C * Lo;
-      // noise conv: X = noise_conv(har)
-      {
-        DirectConvArgs d{};
-        d.x = har; d.xb = N; d.xc = N;
-        d.w = stages[i].nw; d.bias = stages[i].nb;
-        d.out = X; d.ob = CL; d.oc = Lo;
-        d.C_in = 1; d.C_out = C; d.L_in = (int)N;
-        d.n_out = (int)((N + 2 * (noise_s[i] / 2) - noise_k[i]) / noise_s[i] + 1);
-        RVC_CHECK(d.n_out == Lo, "noise conv length does not match the upsampled length");
-        d.K = noise_k[i]; d.stride = noise_s[i]; d.dil = 1; d.in_off = -(noise_s[i] / 2);
-        d.combine = COMB_STORE; d.div = 1.f; d.B = B;
-        std::snprintf(tg, sizeof tg, "dec.noise.s%d", i);
-        run(tg, 2.0 * B * CL * noise_k[i], 4.0 * B * ((double)N + CL), [&] { launch_conv1d_direct(d, s); });
-      }
+      float* X = dec_noise[i];
       // ups: X += ConvTranspose1d(lrelu(cur, 0.1)) + bias
       {
         const int K = kernels[i], st = rates[i], pad = (K - st) / 2;
@@ -607,9 +663,10 @@ int32_t rvc_synth_infer_dev(int64_t sh, int64_t phone, int64_t pitch, int64_t ns
     const float* nsp = e.fptr(ns, B * P * s.upp, "infer ns");
     float* wv = e.fptr(wave, B * P * s.upp, "infer wave");
     float* g = s.buf("g", (size_t)B * s.gin);
-    const float* z = s.enc_flow(ph, static_cast<const long long*>(pb.ptr), static_cast<const long long*>(sb.ptr), nzp,
-                                (int)B, (int)P, g);
-    s.decode(z, (long long)s.H * P, g, f0, nsp, (int)B, (int)P, wv);
+    s.speaker(static_cast<const long long*>(sb.ptr), (int)B, g);
+    s.decode_prep(g, f0, nsp, (int)B, (int)P);
+    const float* z = s.enc_flow(ph, static_cast<const long long*>(pb.ptr), nzp, (int)B, (int)P, g);
+    s.decode_main(z, (long long)s.H * P, (int)B, (int)P, wv);
     e.sync();
     s.collect_timing();
   });
@@ -640,9 +697,10 @@ int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, co
     RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
     float* g = s.buf("g", (size_t)B * s.gin);
-    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch),
-                                reinterpret_cast<const long long*>(d_sid), d_nz, (int)B, (int)P, g);
-    s.decode(z, (long long)s.H * P, g, d_f0, d_ns, (int)B, (int)P, d_w);
+    s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
+    s.decode_prep(g, d_f0, d_ns, (int)B, (int)P);
+    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g);
+    s.decode_main(z, (long long)s.H * P, (int)B, (int)P, d_w);
     RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
     s.collect_timing();
