@@ -181,19 +181,30 @@ int64_t rvc_mem_top(int64_t h, int64_t n, int64_t* out);
  * device), NUL-terminated; -1 if buf_size is too small */
 int32_t rvc_probe_extensions(int64_t h, char* buf, int64_t buf_size);
 
-/* ---------------------------------------------------------------- not provided
- * Exported so the reference's loader (runtime/_vulkan.py:148-278 binds every
- * symbol) can load this library; each returns -1 with a message.  They serve
- * the RMVPE pitch model and training, outside the synthesis path:
- * rvc_matmul_f16 (ffi.zig:246), rvc_conv2d (:378), rvc_conv_t2d (:428),
- * rvc_insert_zeros_2x (:483), rvc_batch_add_conv2d (:1196),
- * rvc_batch_add_conv_t2d (:1246), rvc_batch_add_im2col_1d (:1304),
- * rvc_batch_add_im2col_2d (:1341), rvc_batch_add_gru (:1377), rvc_gru (:1394),
- * rvc_batch_add_gru_sync (:1411). */
-int32_t rvc_matmul_f16(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* ---------------------------------------------------------------- RMVPE ops
+ * rvc_conv2d (engine/src/ffi.zig:378): out[B][C_out][OH][OW] = conv2d(x[B][C_in]
+ * [ih][iw], w[C_out][C_in][kh][kw]) + b (b == 0: none), symmetric padding,
+ * dilation 1; on this backend kh, kw <= 3 and stride_h == stride_w in {1, 2}
+ * (RMVPE's 3x3 / 1x1 convs and the 2x2 stride-2 pooling conv), other shapes
+ * return -1 with a message.
+ * rvc_gru (ffi.zig:1394, engine.zig:3097): bidirectional GRU recurrence, a =
+ * gate inputs [2T][3H] (forward rows then reverse rows, time order), b = W_hh
+ * [2][3H][H], c = b_hh [2][3H], out [T][2H]; H <= 256. */
 int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t ih,
                    int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h, int64_t pad_w, int64_t stride_h,
                    int64_t stride_w);
+int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
+
+/* ---------------------------------------------------------------- not provided
+ * Exported so the reference's loader (runtime/_vulkan.py:148-278 binds every
+ * symbol) can load this library; each returns -1 with a message.  They serve
+ * training and the reference's record/commit form of the RMVPE ops:
+ * rvc_matmul_f16 (ffi.zig:246), rvc_conv_t2d (:428), rvc_insert_zeros_2x (:483),
+ * rvc_batch_add_conv2d (:1196), rvc_batch_add_conv_t2d (:1246),
+ * rvc_batch_add_im2col_1d (:1304), rvc_batch_add_im2col_2d (:1341),
+ * rvc_batch_add_gru (:1377), rvc_batch_add_gru_sync (:1411).  RMVPE as a whole
+ * runs in the rvc_rmvpe_* session below. */
+int32_t rvc_matmul_f16(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
 int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, int64_t c_in, int64_t ih, int64_t iw,
                      int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                      int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out);
@@ -211,7 +222,6 @@ int32_t rvc_batch_add_im2col_2d(int64_t h, int64_t x, int64_t out, int64_t B, in
                                 int64_t oh, int64_t ow, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
                                 int64_t pw);
 int32_t rvc_batch_add_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
-int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
 int32_t rvc_batch_add_gru_sync(int64_t h, int64_t a, int64_t t, int64_t hdim);
 
 /* ---------------------------------------------------------------- synthesis session
@@ -281,6 +291,31 @@ int32_t rvc_hubert_read(int64_t s, const char* name, float* dst, int64_t n);
 int32_t rvc_hubert_set_debug(int64_t s, int32_t keep);
 int32_t rvc_hubert_set_timing(int64_t s, const char* tag);
 int32_t rvc_hubert_get_timing(int64_t s, double* total_ms, int64_t* launches, double* flops, double* bytes);
+
+/* ---------------------------------------------------------------- RMVPE session
+ * No counterpart in the reference ABI.  A device-resident RMVPE pitch
+ * extractor: RMVPE.infer_from_audio (runtime/models/rmvpe.py:927-952) -- log-mel
+ * front end (:632-640), the U-Net of ConvBlockRes levels (:643-690), cnn, BiGRU,
+ * Linear + sigmoid (:727-751) and the local-average cents decode (:899-924) --
+ * as one stream of HIP kernels over weights uploaded once.  Weights are
+ * registered under the rmvpe.pt state-dict keys; BatchNorm is folded into the
+ * convolutions at finalize. */
+int64_t rvc_rmvpe_create(int64_t h);
+int32_t rvc_rmvpe_destroy(int64_t r);
+int32_t rvc_rmvpe_set_weight(int64_t r, const char* key, const float* data, const int64_t* shape, int32_t ndim);
+int32_t rvc_rmvpe_finalize(int64_t r);
+/* STFT frames F = 1 + T / 160 for T samples (runtime/dsp/fft.py:102). */
+int32_t rvc_rmvpe_frames(int64_t r, int64_t T, int64_t* F);
+/* audio [T] float32 16 kHz (T > 512) -> f0 [F] Hz, 0 where the salience
+ * maximum is <= thred (infer_from_audio(x, thred)). */
+int32_t rvc_rmvpe_infer(int64_t r, const float* x, int64_t T, double thred, float* f0);
+int32_t rvc_rmvpe_infer_dev(int64_t r, int64_t x, int64_t T, double thred, int64_t f0);
+/* Named intermediates of the last call: "mel" [128][F] log-mel, "salience"
+ * [360][F'] (F' = F rounded up to a multiple of 32; mel2hidden is its
+ * transpose cut to F frames), "gru_in" [384][F'], "gru_out" [512][F']. */
+int32_t rvc_rmvpe_read(int64_t r, const char* name, float* dst, int64_t n);
+int32_t rvc_rmvpe_set_timing(int64_t r, const char* tag);
+int32_t rvc_rmvpe_get_timing(int64_t r, double* total_ms, int64_t* launches, double* flops, double* bytes);
 
 /* ---------------------------------------------------------------- conversion glue session
  * No counterpart in the reference ABI.  The steps of runtime/pipeline.py either

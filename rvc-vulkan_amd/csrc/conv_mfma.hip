@@ -57,6 +57,7 @@ __device__ __forceinline__ float apply_act(float v, int act, float slope) {
   if (act == ACT_TANH) return tanhf(v);
   if (act == ACT_RELU) return fmaxf(v, 0.f);
   if (act == ACT_GELU) return gelu_as(v);
+  if (act == ACT_SIGMOID) return sigmoid_as(v);
   return v;
 }
 

@@ -1101,9 +1101,55 @@ static int32_t not_provided(const char* name) {
 int32_t rvc_matmul_f16(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
   return not_provided("rvc_matmul_f16");
 }
-int32_t rvc_conv2d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                   int64_t, int64_t, int64_t, int64_t, int64_t) {
-  return not_provided("rvc_conv2d");
+// engine/src/ffi.zig:378-426 + engine.zig:1602-1660: out[B][C_out][OH][OW] =
+// conv2d(x[B][C_in][H][W], w[C_out][C_in][KH][KW]) + b (b == 0: none), symmetric
+// zero padding, dilation 1.  The MFMA kernel takes kernels up to 3x3 and one
+// stride of 1 or 2 on both axes (RMVPE's 3x3 / 1x1 convs and the 2x2 stride-2
+// pooling conv); other shapes are rejected with a message.
+int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t H,
+                   int64_t W, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h, int64_t pad_w, int64_t stride_h,
+                   int64_t stride_w) {
+  return guarded(h, [&](Engine& e) {
+    RVC_CHECK(B >= 1 && c_in >= 1 && H >= 1 && W >= 1 && c_out >= 1 && kh >= 1 && kw >= 1 && pad_h >= 0 &&
+                  pad_w >= 0 && stride_h >= 1 && stride_w >= 1,
+              "conv2d: invalid dimensions");
+    RVC_CHECK(kh <= H + 2 * pad_h && kw <= W + 2 * pad_w, "conv2d: kernel must fit the padded extent");
+    RVC_CHECK(kh <= 3 && kw <= 3 && stride_h == stride_w && stride_h <= 2,
+              "conv2d: this backend takes kernels up to 3x3 and one stride of 1 or 2 on both axes");
+    RVC_CHECK(B * c_in * H * W < (1LL << 40) && c_in <= (1 << 20) && c_out <= (1 << 20), "conv2d: too large");
+    const long long OH = (H + 2 * pad_h - kh) / stride_h + 1, OW = (W + 2 * pad_w - kw) / stride_w + 1;
+    const float* xp = e.fptr(x, B * c_in * H * W, "conv2d x");
+    const float* wp = e.fptr(w, c_out * c_in * kh * kw, "conv2d w");
+    const float* bp = b ? e.fptr(b, c_out, "conv2d b") : nullptr;
+    float* op = e.fptr(out, B * c_out * OH * OW, "conv2d out");
+    Conv2dLaunch a{};
+    a.n_groups = 1;
+    Conv2dGroup& g = a.g[0];
+    g.ntaps = (int)(kh * kw);
+    for (int i = 0; i < kh; ++i)
+      for (int j = 0; j < kw; ++j) {
+        g.dh[i * kw + j] = i - (int)pad_h;
+        g.dw[i * kw + j] = j - (int)pad_w;
+      }
+    g.a_lim = (int)OH;
+    g.b_lim = (int)OW;
+    a.x = xp; a.xb = c_in * H * W; a.xc = H * W; a.H = (int)H; a.W = (int)W;
+    a.out = op; a.ob = c_out * OH * OW; a.oc = OH * OW; a.ors = OW; a.ocs = 1;
+    a.bias = bp; a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
+    a.OH = (int)OH; a.OW = (int)OW; a.osh = a.osw = 1; a.stride = (int)stride_h;
+    const size_t wfl = (size_t)kh * kw * c_in * a.w_ld;
+    const size_t need = conv2d_split_floats(a);
+    float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (wfl + need)));
+    g.w = sc;
+    if (need > 0) {
+      a.part = sc + wfl;
+      a.part_floats = need;
+    }
+    submit(e, [&] {
+      launch_pack_conv2d_weight(wp, sc, (int)c_out, (int)c_in, (int)kh, (int)kw, e.stream);
+      launch_conv2d(a, e.stream);
+    });
+  });
 }
 int32_t rvc_conv_t2d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                      int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
@@ -1132,7 +1178,32 @@ int32_t rvc_batch_add_im2col_2d(int64_t, int64_t, int64_t, int64_t, int64_t, int
 int32_t rvc_batch_add_gru(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
   return not_provided("rvc_batch_add_gru");
 }
-int32_t rvc_gru(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) { return not_provided("rvc_gru"); }
+// engine/src/ffi.zig:1394-1409 + engine.zig:3097-3112: bidirectional GRU
+// recurrence over precomputed gate inputs a [2T][3H] (rows 0..T-1 forward,
+// T..2T-1 reverse, both in time order), weights b = W_hh [2][3H][H], c = b_hh
+// [2][3H]; out [T][2H] (forward units first).  H <= 256 as in the reference.
+int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim) {
+  return guarded(h, [&](Engine& e) {
+    RVC_CHECK(t >= 1 && hdim >= 1 && hdim <= 256 && t < (1LL << 30), "gru: need T >= 1 and 1 <= H <= 256");
+    const long long k = 3 * hdim;
+    GruArgs g{};
+    g.gx = e.fptr(a, 2 * t * k, "gru gx");
+    g.whh = e.fptr(b, 2 * k * hdim, "gru w_hh");
+    g.bhh = e.fptr(c, 2 * k, "gru b_hh");
+    g.out = e.fptr(out, t * 2 * hdim, "gru out");
+    g.g_d = t * k; g.g_t = k; g.g_r = 1;
+    g.o_d = hdim; g.o_t = 2 * hdim; g.o_j = 1;
+    g.T = (int)t; g.H = (int)hdim; g.spin_limit = 1LL << 22;
+    float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (2 * 2 * 256 + 4)));
+    g.state = sc;
+    g.sync = reinterpret_cast<unsigned*>(sc + 2 * 2 * 256);
+    submit(e, [&] { launch_bigru(g, e.stream); });
+    unsigned flag = 0;
+    RVC_HIP(hipMemcpyAsync(&flag, g.sync + 2, sizeof(unsigned), hipMemcpyDeviceToHost, e.stream));
+    e.sync();
+    RVC_CHECK(flag == 0, "gru: step barrier timed out (workgroups not co-resident)");
+  });
+}
 int32_t rvc_batch_add_gru_sync(int64_t, int64_t, int64_t, int64_t) { return not_provided("rvc_batch_add_gru_sync"); }
 
 }  // extern "C"

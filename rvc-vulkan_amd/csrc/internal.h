@@ -43,7 +43,14 @@ void check_launch(const char* what);
 // ---------------------------------------------------------------- conv args
 // Activation applied while loading an input tile (prologue) or before the
 // combine step of the epilogue.
-enum Act : int { ACT_NONE = 0, ACT_LEAKY = 1, ACT_TANH = 2, ACT_RELU = 3, ACT_GELU = 4 };
+enum Act : int { ACT_NONE = 0, ACT_LEAKY = 1, ACT_TANH = 2, ACT_RELU = 3, ACT_GELU = 4, ACT_SIGMOID = 5 };
+
+// logistic function in the two-branch form of runtime/nn.py:520-523
+__device__ inline float sigmoid_as(float x) {
+  if (x >= 0.f) return 1.0f / (1.0f + expf(-x));
+  const float e = expf(x);
+  return e / (1.0f + e);
+}
 
 // GELU with erf by Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), the
 // formula and float32 operation order of the reference's numpy gelu_erf
@@ -299,5 +306,62 @@ void launch_attn_context(const float* w, const float* v, const float* used, floa
 // ---------------------------------------------------------------- matmul
 // c[M][N] = a[M][K] @ b[K][N], row-major (op-level rvc_matmul)
 void launch_matmul(const float* a, const float* b, float* c, int M, int K, int N, hipStream_t s);
+
+// ------------------------------------------------------------------ conv2d
+// Implicit-GEMM 2-D convolution on fp32 MFMA (csrc/rmvpe.hip).  Computed
+// point (a, b) of group g (a < OH, b < OW) sums, over taps t and input
+// channels ci, w_t[ci][co] * x[ci][a*stride + dh_t][b*stride + dw_t] (zero
+// outside [0, H) x [0, W)); points with a >= a_lim or b >= b_lim take no taps.
+// v = acc + bias; relu; + res; stored at
+//   out[b*ob + co*oc + (a*osh + oh0)*ors + (b*osw + ow0)*ocs]  (res alike).
+constexpr int kConv2dTapsMax = 9;
+constexpr int kConv2dGroupsMax = 4;
+struct Conv2dGroup {
+  const float* w;  // packed [ntaps][C_in][w_ld], 16-byte aligned
+  int ntaps;
+  int dh[kConv2dTapsMax], dw[kConv2dTapsMax];
+  int oh0, ow0;
+  int a_lim, b_lim;
+  int dh_lo, dw_lo, dh_span, dw_span;  // set by the launcher
+};
+struct Conv2dLaunch {
+  Conv2dGroup g[kConv2dGroupsMax];
+  int n_groups;
+  const float* x; long long xb, xc; int H, W;   // input [B][C_in (stride xc)][H][W]
+  float* out; long long ob, oc, ors, ocs;
+  const float* res;
+  const float* bias;
+  int relu;
+  int C_in, C_out, w_ld, B;
+  int OH, OW, osh, osw;
+  int stride;                                   // 1 or 2 on both axes
+  float* part; size_t part_floats;              // split-K scratch (optional)
+  int ksplit, csplit, tile_c;                   // set by the launcher
+};
+size_t conv2d_split_floats(const Conv2dLaunch& a);
+void launch_conv2d(const Conv2dLaunch& a, hipStream_t s);
+// host-side packing: [C_out][C_in][KH][KW] (times scale[co] when given) ->
+// [KH*KW][C_in][packed_ld(C_out)], tap t = kh*KW + kw
+std::vector<float> pack_conv2d_host(const float* w, const float* scale, int C_out, int C_in, int KH, int KW);
+void launch_pack_conv2d_weight(const float* w, float* out, int C_out, int C_in, int KH, int KW, hipStream_t s);
+void launch_avg_pool2(const float* x, float* out, int BC, int H, int W, hipStream_t s);
+
+// ------------------------------------------------------------------ RMVPE
+void launch_rmvpe_blocks(const float* x, int T, float* xb, int NB, hipStream_t s);
+void launch_mel_mag(const float* S, float* mag, int nbin, int F, hipStream_t s);
+void launch_logmel_image(const float* M, int F, int Fp, int n_mels, float bn_s, float bn_t, float* img,
+                         float* logmel, hipStream_t s);
+struct GruArgs {
+  const float* gx;  long long g_d, g_t, g_r;   // gate input of (direction, step, gate row)
+  const float* whh; const float* bhh;          // [2][3H][H], [2][3H]
+  float* out;       long long o_d, o_t, o_j;   // h of (direction, step, unit)
+  float* state;                                 // [2][2][256] hidden-state double buffer
+  unsigned* sync;                               // [4]: arrivals per direction, error flag
+  int T, H;
+  long long spin_limit;
+};
+void launch_bigru(const GruArgs& g, hipStream_t s);
+void launch_rmvpe_decode(const float* sal, long long s_f, long long s_k, int F, int nb, const float* cents,
+                         float thred, float* f0, hipStream_t s);
 
 }  // namespace rvc

@@ -131,6 +131,16 @@ SYMBOLS = {
     "rvc_hubert_set_timing": (I32, [I64, CHARP]),
     "rvc_hubert_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL),
                                     ctypes.POINTER(DBL)]),
+    "rvc_rmvpe_create": (I64, [I64]),
+    "rvc_rmvpe_destroy": (I32, [I64]),
+    "rvc_rmvpe_set_weight": (I32, [I64, CHARP, F32P, I64P, I32]),
+    "rvc_rmvpe_finalize": (I32, [I64]),
+    "rvc_rmvpe_frames": (I32, [I64, I64, I64P]),
+    "rvc_rmvpe_infer": (I32, [I64, F32P, I64, DBL, F32P]),
+    "rvc_rmvpe_infer_dev": (I32, [I64, I64, I64, DBL, I64]),
+    "rvc_rmvpe_read": (I32, [I64, CHARP, F32P, I64]),
+    "rvc_rmvpe_set_timing": (I32, [I64, CHARP]),
+    "rvc_rmvpe_get_timing": (I32, [I64, ctypes.POINTER(DBL), I64P, ctypes.POINTER(DBL), ctypes.POINTER(DBL)]),
     "rvc_vc_create": (I64, [I64]),
     "rvc_vc_destroy": (I32, [I64]),
     "rvc_vc_set_index": (I32, [I64, F32P, I64, I64]),

@@ -41,6 +41,8 @@ __all__ = [
     "load_synthesizer",
     "hubert_state_dict",
     "load_hubert",
+    "rmvpe_state_dict",
+    "load_rmvpe",
 ]
 
 
@@ -296,3 +298,22 @@ def load_hubert(path, ctx=None):
     if os.path.isdir(p):
         p = os.path.join(p, "pytorch_model.bin")
     return HipHubert(hubert_state_dict(load_pth(p)), ctx=ctx)
+
+
+def rmvpe_state_dict(obj):
+    """Float32 state dict of a loaded ``rmvpe.pt`` (fp16 storage cast to
+    float32 as ``runtime/models/rmvpe.py:557-563`` does; the integer
+    ``num_batches_tracked`` counters are dropped)."""
+    sd = obj.get("state_dict", obj.get("model", obj)) if isinstance(obj, dict) else obj
+    if not isinstance(sd, dict):
+        raise CheckpointError("checkpoint holds no state dict")
+    return {str(k): np.asarray(v, dtype=np.float32, order="C") for k, v in sd.items()
+            if isinstance(v, np.ndarray) and not str(k).endswith("num_batches_tracked")}
+
+
+def load_rmvpe(path, ctx=None):
+    """A device-resident ``HipRMVPE`` from ``rmvpe.pt`` (``load_rmvpe``,
+    ``runtime/models/rmvpe.py:955-966``, with the path given)."""
+    from .rmvpe import HipRMVPE
+
+    return HipRMVPE(rmvpe_state_dict(load_pth(os.fspath(path))), ctx=ctx)

@@ -364,3 +364,90 @@ def make_hubert_input(T: int, seed: int) -> np.ndarray:
     """BASELINE config 3 input: x ~ N(0, 0.1) [1, T] at 16 kHz."""
     rng = np.random.default_rng(seed)
     return (0.1 * rng.standard_normal((1, T))).astype(np.float32)
+
+
+# ---------------------------------------------------------------------- RMVPE
+RMVPE_EN = (16, 32, 64, 128, 256)   # encoder level widths (E2E en_out_channels=16, 5 levels)
+RMVPE_INTER = 512                   # intermediate width (4 levels)
+RMVPE_GRU = 256                     # BiGRU hidden size
+RMVPE_BINS = 360
+
+
+def rmvpe_blocks():
+    """(prefix, C_in, C_out) of every ConvBlockRes of ``E2E(4, 1, (2, 2))``
+    in execution order, and (prefix, C_in, C_out) of the five decoder
+    ConvTranspose2d layers (``runtime/models/rmvpe.py:643-690``)."""
+    blocks, ups = [], []
+    c = 1
+    for i, o in enumerate(RMVPE_EN):
+        for j in range(4):
+            blocks.append((f"unet.encoder.layers.{i}.conv.{j}", c if j == 0 else o, o))
+        c = o
+    for i in range(4):
+        for j in range(4):
+            blocks.append((f"unet.intermediate.layers.{i}.conv.{j}", c if j == 0 else RMVPE_INTER, RMVPE_INTER))
+        c = RMVPE_INTER
+    for i in range(5):
+        o = c // 2
+        ups.append((f"unet.decoder.layers.{i}", c, o))
+        for j in range(4):
+            blocks.append((f"unet.decoder.layers.{i}.conv2.{j}", 2 * o if j == 0 else o, o))
+        c = o
+    return blocks, ups
+
+
+def make_rmvpe_weights(seed: int = 0) -> dict:
+    """Random-init float32 RMVPE state dict with the checkpoint's key names
+    (``runtime/models/rmvpe.py:518-551, 643-690, 727-751``).
+
+    Convs and linears: ``U(+-1/sqrt(fan_in))`` (PyTorch's default bound);
+    BatchNorm: gamma ~ U(0.8, 1.2), beta and running_mean ~ U(-0.1, 0.1),
+    running_var ~ U(0.8, 1.2), so each folded scale/shift differs from the
+    identity; GRU: ``U(+-1/sqrt(hidden))`` as ``torch.nn.GRU`` initialises."""
+    rng = np.random.default_rng(seed)
+    w: dict = {}
+
+    def bn(p, n):
+        w[p + ".weight"] = rng.uniform(0.8, 1.2, n).astype(np.float32)
+        w[p + ".bias"] = rng.uniform(-0.1, 0.1, n).astype(np.float32)
+        w[p + ".running_mean"] = rng.uniform(-0.1, 0.1, n).astype(np.float32)
+        w[p + ".running_var"] = rng.uniform(0.8, 1.2, n).astype(np.float32)
+
+    bn("unet.encoder.bn", 1)
+    blocks, ups = rmvpe_blocks()
+    up_at = {p + ".conv2.0": (p, ci, co) for p, ci, co in ups}
+    for p, ci, co in blocks:
+        if p in up_at:
+            q, uci, uco = up_at[p]
+            w[q + ".conv1.0.weight"] = _uniform(rng, (uci, uco, 3, 3), uco * 9)
+            bn(q + ".conv1.1", uco)
+        w[p + ".conv.0.weight"] = _uniform(rng, (co, ci, 3, 3), ci * 9)
+        bn(p + ".conv.1", co)
+        w[p + ".conv.3.weight"] = _uniform(rng, (co, co, 3, 3), co * 9)
+        bn(p + ".conv.4", co)
+        if ci != co:
+            w[p + ".shortcut.weight"] = _uniform(rng, (co, ci, 1, 1), ci)
+            w[p + ".shortcut.bias"] = _uniform(rng, (co,), ci)
+    w["cnn.weight"] = _uniform(rng, (3, RMVPE_EN[0], 3, 3), RMVPE_EN[0] * 9)
+    w["cnn.bias"] = _uniform(rng, (3,), RMVPE_EN[0] * 9)
+    H = RMVPE_GRU
+    for sfx in ("", "_reverse"):
+        w["fc.0.gru.weight_ih_l0" + sfx] = _uniform(rng, (3 * H, 3 * 128), H)
+        w["fc.0.gru.weight_hh_l0" + sfx] = _uniform(rng, (3 * H, H), H)
+        w["fc.0.gru.bias_ih_l0" + sfx] = _uniform(rng, (3 * H,), H)
+        w["fc.0.gru.bias_hh_l0" + sfx] = _uniform(rng, (3 * H,), H)
+    w["fc.1.weight"] = _uniform(rng, (RMVPE_BINS, 2 * H), 2 * H)
+    w["fc.1.bias"] = _uniform(rng, (RMVPE_BINS,), 2 * H)
+    return w
+
+
+def make_rmvpe_audio(T: int, seed: int) -> np.ndarray:
+    """16 kHz test signal: a 110-330 Hz glide plus its 2nd harmonic, noise
+    at -30 dB and a silent gap (exercises the clamp of the log-mel)."""
+    rng = np.random.default_rng(seed)
+    t = np.arange(T) / 16000.0
+    f = 110.0 + 220.0 * t / max(t[-1], 1e-9)
+    ph = 2 * np.pi * np.cumsum(f) / 16000.0
+    x = 0.3 * np.sin(ph) + 0.1 * np.sin(2 * ph) + 0.01 * rng.standard_normal(T)
+    x[T // 3: T // 3 + T // 10] = 0.0
+    return x.astype(np.float32)

@@ -1,0 +1,222 @@
+# -*- coding: utf-8 -*-
+"""GPU parity of RMVPE (``rvc_rmvpe_*`` session, ``rvc_conv2d``, ``rvc_gru``)
+against the oracle (``oracle/rmvpe_ref.py``) and the reference's golden
+vectors.
+
+Bar: per-op relative L2 <= 1e-4 in fp32 (log-mel, the cnn output feeding the
+GRU, the GRU output, the salience); f0 within relative 1e-4 on every frame
+whose salience argmax is not decided by rounding (top-2 gap > 1e-4 in the
+oracle), and those frames must be at least 90 % of the clip.  The decode
+kernel on identical salience matches the oracle to float32 rounding of powf."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle import rmvpe_ref as R
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "rmvpe.npz")
+OP_TOL = 1e-4
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def clear_frames(sal):
+    s = np.sort(np.asarray(sal), axis=1)
+    return (s[:, -1] - s[:, -2]) > 1e-4
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(GOLD, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="module")
+def weights(gold):
+    from rvc_hip import synthetic as syn
+
+    w = syn.make_rmvpe_weights(int(gold["wseed"]))
+    assert syn.weights_digest(w) == str(gold["weights_digest"])
+    return w
+
+
+@pytest.fixture(scope="module")
+def hr(weights):
+    from rvc_hip import _hip
+
+    if not _hip.has_so:
+        pytest.fail(f"HIP backend missing: {_hip.so_load_error}")
+    from rvc_hip.rmvpe import HipRMVPE
+
+    m = HipRMVPE(weights)
+    yield m
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def oracle(weights):
+    return R.Rmvpe(weights)
+
+
+@pytest.mark.parametrize("clip", [0, 1])
+def test_rmvpe_golden(hr, gold, clip):
+    x = gold[f"x{clip}"]
+    print(f"rmvpe golden clip {clip} T={len(x)}", flush=True)
+    f0 = hr.infer_from_audio(x)
+    assert f0.shape == gold[f"f0_{clip}"].shape and f0.dtype == np.float32
+    assert rel_l2(hr.last_mel(), gold[f"mel{clip}"]) < OP_TOL
+    hid = hr.last_hidden()[0]
+    assert hid.shape == gold[f"hidden{clip}"].shape
+    assert rel_l2(hid, gold[f"hidden{clip}"]) < OP_TOL
+    ok = clear_frames(gold[f"hidden{clip}"])
+    assert ok.mean() > 0.9
+    np.testing.assert_allclose(f0[ok], gold[f"f0_{clip}"][ok], rtol=1e-4)
+
+
+def test_rmvpe_vs_oracle_3s(hr, oracle):
+    """3 s clip: F = 301 frames padded to 320 (deep levels of 10 x 4 points,
+    split-K convolutions); each stage against the oracle."""
+    from rvc_hip import synthetic as syn
+
+    x = syn.make_rmvpe_audio(48000, 7)
+    print("rmvpe vs oracle T=48000", flush=True)
+    f0 = hr.infer_from_audio(x)
+    F = R.n_frames(len(x))
+    Fp = 32 * ((F - 1) // 32 + 1)
+    mel = oracle.mel(x)
+    assert rel_l2(hr.last_mel(), mel) < OP_TOL
+    melp = np.pad(mel[None], ((0, 0), (0, 0), (0, Fp - F)))
+    cnn = oracle.unet_cnn(melp.transpose(0, 2, 1)[:, None])             # [1, 3, Fp, 128]
+    gin = cnn.transpose(0, 2, 1, 3).reshape(Fp, -1).T                   # [384, Fp]
+    assert rel_l2(hr.read("gru_in", gin.shape), gin) < OP_TOL
+    sal = oracle.hidden_from_cnn(cnn)[0]                                  # [Fp, 360]
+    got = hr.read("salience", (sal.shape[1], Fp)).T
+    assert rel_l2(got, sal) < OP_TOL
+    ok = clear_frames(sal[:F])
+    assert ok.mean() > 0.9
+    np.testing.assert_allclose(f0[ok], R.decode(sal[:F])[ok], rtol=1e-4)
+
+
+def test_rmvpe_silence_and_short_input(hr, oracle):
+    """All-zero audio (every log-mel clamped) and the shortest legal input."""
+    for x in (np.zeros(3200, np.float32), (0.1 * np.random.default_rng(3).standard_normal(513)).astype(np.float32)):
+        print(f"rmvpe T={len(x)}", flush=True)
+        f0 = hr.infer_from_audio(x)
+        ref = oracle.infer_from_audio(x)
+        assert f0.shape == ref.shape
+        sal = oracle.mel2hidden(oracle.mel(x)[None])[0]
+        assert rel_l2(hr.last_hidden()[0], sal) < OP_TOL
+        ok = clear_frames(sal)
+        np.testing.assert_allclose(f0[ok], ref[ok], rtol=1e-4)
+    from rvc_hip import _hip
+
+    with pytest.raises(RuntimeError, match="512"):
+        hr.infer_from_audio(np.zeros(512, np.float32))
+    assert "512" in _hip.last_error()
+
+
+def _ctx():
+    from rvc_hip.hip_ops import get_context
+
+    return get_context()
+
+
+@pytest.mark.parametrize("B,C_in,H,W,C_out,k,pad,stride", [
+    (1, 16, 64, 128, 16, 3, 1, 1),      # encoder level 0 shape
+    (1, 1, 32, 128, 16, 3, 1, 1),       # the first conv (one input channel)
+    (2, 40, 9, 13, 24, 3, 1, 1),        # ragged: odd extents, partial tiles
+    (1, 512, 8, 4, 512, 3, 1, 1),       # intermediate level: split-K
+    (1, 64, 16, 8, 96, 1, 0, 1),        # 1x1 shortcut
+    (1, 32, 20, 16, 32, 2, 0, 2),       # 2x2 stride-2 pooling conv
+])
+def test_conv2d_export_vs_oracle(B, C_in, H, W, C_out, k, pad, stride):
+    from rvc_hip import _hip
+
+    ctx = _ctx()
+    L = _hip.get_lib()
+    rng = np.random.default_rng(C_in * 7 + H)
+    x = rng.standard_normal((B, C_in, H, W)).astype(np.float32)
+    w = (rng.standard_normal((C_out, C_in, k, k)) / np.sqrt(C_in * k * k)).astype(np.float32)
+    b = rng.standard_normal(C_out).astype(np.float32)
+    OH, OW = (H + 2 * pad - k) // stride + 1, (W + 2 * pad - k) // stride + 1
+    if stride == 1:
+        ref = R.conv2d(x, w, b, pad)
+    else:
+        full = R.conv2d(x, w, b, pad)
+        ref = full[:, :, ::stride, ::stride][:, :, :OH, :OW]
+    ids = [ctx.upload(x), ctx.upload(w), ctx.upload(b), ctx.alloc(B * C_out * OH * OW)]
+    try:
+        print(f"conv2d {B}x{C_in}x{H}x{W} -> {C_out} k{k} s{stride}", flush=True)
+        _hip._check(L.rvc_conv2d(ctx.handle, ids[0], ids[1], ids[2], ids[3], B, C_in, H, W, C_out, k, k, pad, pad,
+                                 stride, stride), "rvc_conv2d")
+        got = ctx.download(ids[3], (B, C_out, OH, OW))
+    finally:
+        for i in ids:
+            ctx.free(i)
+    assert rel_l2(got, ref) < OP_TOL
+
+
+def test_conv2d_export_rejects_unsupported():
+    from rvc_hip import _hip
+
+    ctx = _ctx()
+    L = _hip.get_lib()
+    ids = [ctx.alloc(4096) for _ in range(3)]
+    try:
+        assert L.rvc_conv2d(ctx.handle, ids[0], ids[1], 0, ids[2], 1, 1, 16, 16, 1, 5, 5, 2, 2, 1, 1) == -1
+        assert "3x3" in _hip.last_error()
+        assert L.rvc_conv2d(ctx.handle, ids[0], ids[1], 0, ids[2], 1, 1, 16, 16, 1, 3, 3, 1, 1, 1, 2) == -1
+    finally:
+        for i in ids:
+            ctx.free(i)
+
+
+@pytest.mark.parametrize("T,I,H", [(37, 24, 16), (200, 384, 256), (5, 8, 100)])
+def test_gru_export_vs_oracle(T, I, H):
+    """rvc_gru on the reference's layout: gate inputs [2T][3H] from
+    x @ W_ih^T + b_ih of each direction, W_hh [2][3H][H], b_hh [2][3H]."""
+    from rvc_hip import _hip
+
+    ctx = _ctx()
+    L = _hip.get_lib()
+    rng = np.random.default_rng(T + H)
+    bound = 1.0 / np.sqrt(H)
+    p = {k: rng.uniform(-bound, bound, s).astype(np.float32) for k, s in (
+        ("wi", (3 * H, I)), ("wh", (3 * H, H)), ("bi", (3 * H,)), ("bh", (3 * H,)),
+        ("wir", (3 * H, I)), ("whr", (3 * H, H)), ("bir", (3 * H,)), ("bhr", (3 * H,)))}
+    x = rng.standard_normal((T, I)).astype(np.float32)
+    ref = R.bigru(x, p["wi"], p["wh"], p["bi"], p["bh"], p["wir"], p["whr"], p["bir"], p["bhr"])
+    gx = np.concatenate([x @ p["wi"].T + p["bi"], x @ p["wir"].T + p["bir"]], axis=0).astype(np.float32)
+    ids = [ctx.upload(gx), ctx.upload(np.stack([p["wh"], p["whr"]])), ctx.upload(np.stack([p["bh"], p["bhr"]])),
+           ctx.alloc(T * 2 * H)]
+    try:
+        print(f"gru T={T} H={H}", flush=True)
+        _hip._check(L.rvc_gru(ctx.handle, ids[0], ids[1], ids[2], ids[3], T, H), "rvc_gru")
+        got = ctx.download(ids[3], (T, 2 * H))
+    finally:
+        for i in ids:
+            ctx.free(i)
+    assert rel_l2(got, ref) < OP_TOL
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)
+
+
+def test_rmvpe_timing_breakdown(hr):
+    from rvc_hip import synthetic as syn
+
+    x = syn.make_rmvpe_audio(16000, 2)
+    hr.set_timing("rmvpe")
+    hr.infer_from_audio(x)
+    t = hr.timing()
+    hr.set_timing("")
+    assert t["launches"] > 100 and t["ms"] > 0 and t["flops"] > 1e9
