@@ -17,7 +17,8 @@ encoder, 10 s of 16 kHz audio -> [1, 499, 768]), ``--workload dec48k-b8``
 config 4 (48k GeneratorNSF, 8 chunks of 6 s as one batch), ``--workload
 synth40k-bf16-b4`` config 5, and ``--workload vc40k`` the device-resident
 conversion chain around config 2 (HuBERT, retrieval, synthesis, RMS mix,
-int16); each prints its own JSON line in the same format.  The default run
+int16), and ``--workload rmvpe10s`` RMVPE pitch extraction of 10 s at
+16 kHz; each prints its own JSON line in the same format.  The default run
 is config 2.
 """
 
@@ -481,10 +482,85 @@ def bench_vc(args):
     return 0
 
 
+def bench_rmvpe(args):
+    """RMVPE f0 extraction (the pipeline's pitch model), 160 000 samples at
+    16 kHz -> f0 [1001], batch 1, fp32, device-resident."""
+    from rvc_hip import _hip, synthetic as syn
+    from rvc_hip.hip_ops import get_context
+    from rvc_hip.rmvpe import HipRMVPE
+
+    T = 160000
+    w = syn.make_rmvpe_weights(seed=0)
+    ctx = get_context()
+    m = HipRMVPE(w, ctx=ctx)
+    _log(f"bench: device {_hip.device_name()}; RMVPE weights resident")
+    x = syn.make_rmvpe_audio(T, seed=5)
+    F = m.frames(T)
+    xid = ctx.upload(x)
+    fid = ctx.alloc(F)
+
+    def step():
+        m.infer_dev(xid, T, fid)
+
+    for _ in range(args.warmup):
+        step()
+    m.set_timing("rmvpe.enc")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dt = time.perf_counter() - t0
+    fam = m.timing()
+    m.set_timing("")
+    breakdown = {}
+    for tag in () if args.quick else ("rmvpe.mel", "rmvpe.enc", "rmvpe.pool", "rmvpe.inter", "rmvpe.dec",
+                                      "rmvpe.head", "rmvpe.gru", "rmvpe.decode"):
+        m.set_timing(tag)
+        step()
+        t = m.timing()
+        breakdown[tag] = {"ms": round(t["ms"], 4), "launches": t["launches"],
+                          "tflops": round(t["flops"] / (t["ms"] / 1e3) / 1e12, 2) if t["ms"] > 0 else None}
+    m.set_timing("")
+    audio_s = T / 16000.0
+    value = audio_s * args.steps / dt
+    n = max(fam["launches"], 1)
+    avg_s = fam["ms"] / 1e3 / n
+    achieved = fam["flops"] / n / avg_s / 1e12 if avg_s > 0 else 0.0
+    roofline = {"kernel": "conv2d_mfma (RMVPE encoder ConvBlockRes 3x3 convs)", "bound": "mfma",
+                "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n // args.steps,
+                "share_of_step": round(fam["ms"] / (dt * 1e3), 3)}
+    cpu = None
+    if not (args.no_cpu_baseline or args.quick):
+        from oracle import rmvpe_ref
+
+        ref = rmvpe_ref.Rmvpe(w)
+        xs = syn.make_rmvpe_audio(16000, seed=7)
+        ref.infer_from_audio(xs[:4000])
+        t0 = time.perf_counter()
+        ref.infer_from_audio(xs)
+        cdt = time.perf_counter() - t0
+        cpu = {"value": 1.0 / cdt, "unit": "audio-s/s", "cores": _blas_threads(), "kind": "port",
+               "sample": f"1 s (16 000 samples) of the same extraction (same weights), numpy oracle, 1 run after "
+                         f"a warm-up, {cdt:.2f} s wall"}
+    line = {
+        "metric": "audio-sec pitch-extracted/sec (RMVPE, 10 s @16 kHz, 1 GPU)", "value": round(value, 2),
+        "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded glide + noise, random-init weights)",
+        "config": {"workload": "rmvpe10s: RMVPE f0, 160000 samples @16 kHz -> f0 [1001], batch 1, fp32",
+                   "samples": T, "frames": F, "batch": 1},
+        "roofline": roofline, "cpu_baseline": cpu, "breakdown": breakdown,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", default="synth40k",
-                    choices=("synth40k", "hubert", "dec48k-b8", "synth40k-bf16-b4", "synth40k-bf16rb-b4", "vc40k"),
+                    choices=("synth40k", "hubert", "dec48k-b8", "synth40k-bf16-b4", "synth40k-bf16rb-b4", "vc40k",
+                             "rmvpe10s"),
                     help="synth40k: BASELINE config 2 (default); hubert: config 3; dec48k-b8: config 4; "
                          "synth40k-bf16-b4: config 5 (ups + enc_p matmuls on bf16); synth40k-bf16rb-b4: config 5 "
                          "with the ResBlocks on bf16 too (reported separately); vc40k: the conversion chain "
@@ -510,6 +586,8 @@ def main():
         return bench_hubert(args)
     if args.workload == "dec48k-b8":
         return bench_dec48(args)
+    if args.workload == "rmvpe10s":
+        return bench_rmvpe(args)
     if args.workload == "vc40k":
         return bench_vc(args)
     if args.workload.startswith("synth40k-bf16"):

@@ -411,7 +411,10 @@ __device__ __forceinline__ void persist_tile(int lin, int n_tx, int n_ty, int& t
   }
 }
 
-template <int BM, int BN, int WM, int WN, int BK>
+// FAM only names the instantiation (1: the three-group stored launches of
+// the decoder ResBlocks), so profiles can tell them from the other launches
+// of the same tile; the code is identical.
+template <int BM, int BN, int WM, int WN, int BK, int FAM>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(4)))
 void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floats) {
@@ -761,14 +764,21 @@ bool launch_persist(const ConvLaunch& a, hipStream_t s) {
   const int n_ty = (a.C_out + BM - 1) / BM;
   const long long items = (long long)a.B * n_tx * n_ty * a.n_groups;
   RVC_CHECK(items < (1LL << 30), "conv1d_mfma: launch too large");
-  const void* kern = reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK>);
+  bool fam = a.n_groups == 3;
+  for (int g = 0; g < a.n_groups; ++g) fam = fam && a.g[g].combine == COMB_STORE;
+  const void* kern = fam ? reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1>)
+                         : reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0>);
   const int per_cu = resident_blocks(kern, C::NT, lds);
   if (per_cu < 1) return false;
   long long grid = (long long)per_cu * device_cus();
   if (grid >= 8) grid -= grid % 8;  // item j then runs on XCD j % 8
   grid = std::min(grid, items);
-  hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK>), dim3((unsigned)grid), dim3(C::NT), lds, s, a,
-                     n_tx, n_ty, stage);
+  if (fam)
+    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1>), dim3((unsigned)grid), dim3(C::NT), lds,
+                       s, a, n_tx, n_ty, stage);
+  else
+    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0>), dim3((unsigned)grid), dim3(C::NT), lds,
+                       s, a, n_tx, n_ty, stage);
   check_launch("conv1d_mfma_persist");
   return true;
 }

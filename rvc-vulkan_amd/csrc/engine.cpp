@@ -1194,7 +1194,7 @@ int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t
     g.g_d = t * k; g.g_t = k; g.g_r = 1;
     g.o_d = hdim; g.o_t = 2 * hdim; g.o_j = 1;
     g.T = (int)t; g.H = (int)hdim; g.spin_limit = 1LL << 22;
-    float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (2 * 2 * 256 + 4)));
+    auto* sc = static_cast<unsigned long long*>(e.scratch_for(sizeof(unsigned long long) * (2 * 2 * 256 + 2)));
     g.state = sc;
     g.sync = reinterpret_cast<unsigned*>(sc + 2 * 2 * 256);
     submit(e, [&] { launch_bigru(g, e.stream); });

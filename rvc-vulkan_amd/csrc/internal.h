@@ -355,7 +355,7 @@ struct GruArgs {
   const float* gx;  long long g_d, g_t, g_r;   // gate input of (direction, step, gate row)
   const float* whh; const float* bhh;          // [2][3H][H], [2][3H]
   float* out;       long long o_d, o_t, o_j;   // h of (direction, step, unit)
-  float* state;                                 // [2][2][256] hidden-state double buffer
+  unsigned long long* state;                    // [2][2][256] tagged hidden-state double buffer
   unsigned* sync;                               // [4]: arrivals per direction, error flag
   int T, H;
   long long spin_limit;

@@ -455,7 +455,7 @@ struct Rmvpe : SessionBase {
     float* GX = buf("gru_gx", (size_t)6 * gru_h * Fp);
     conv("rmvpe.head", c1x1(X, (long long)Cx * Fp, wih, bih, GX, 1, Cx, 6 * gru_h, Fp));
     float* HO = buf("gru_out", (size_t)2 * gru_h * Fp);
-    float* state = buf("gru_state", 2 * 2 * 256);
+    auto* state = reinterpret_cast<unsigned long long*>(buf("gru_state", 2 * 2 * 256 * 2));
     unsigned* sync = reinterpret_cast<unsigned*>(buf("gru_sync", 4));
     {
       GruArgs ga{};

@@ -269,14 +269,29 @@ int pow2_at_least(int v) {
   return p;
 }
 
+long long conv2d_tiles(const Conv2dLaunch& a, const Conv2dCfg& c) {
+  const int tc = std::min(c.BN, pow2_at_least(a.OW));
+  const int tr = c.BN / tc;
+  return (long long)((a.OH + tr - 1) / tr) * ((a.OW + tc - 1) / tc) * ((a.C_out + c.BM - 1) / c.BM) * a.n_groups *
+         a.B;
+}
+
+// Largest tile whose grid still gives every CU a workgroup (256 CUs); the
+// 16-row tile for 16 output channels.  When even 32 x 32 tiles leave CUs
+// idle, the channels are split over workgroups (conv2d_plan).
 Conv2dCfg conv2d_cfg(const Conv2dLaunch& a) {
   if (a.stride == 2) return {32, 64};
   if (a.C_out <= 16) return {16, 256};
-  if (a.C_out <= 32) return {32, 128};
-  return {64, 128};
+  static const Conv2dCfg order[] = {{64, 128}, {32, 128}, {64, 64}, {32, 64}, {32, 32}};
+  for (const Conv2dCfg& c : order) {
+    if (c.BM == 64 && a.C_out <= 32) continue;
+    if (conv2d_tiles(a, c) >= 256) return c;
+  }
+  return {32, 32};
 }
 
-// channel split over workgroups when the tile grid cannot fill the GPU
+// channel split over workgroups when the tile grid cannot fill the GPU:
+// about 512 workgroups, at least 4 chunks of 8 channels per split
 void conv2d_plan(Conv2dLaunch& a, const Conv2dCfg& c, int& n_tiles, int& n_co, int& nz) {
   a.tile_c = std::min(c.BN, pow2_at_least(a.OW));
   const int TR = c.BN / a.tile_c;
@@ -286,9 +301,9 @@ void conv2d_plan(Conv2dLaunch& a, const Conv2dCfg& c, int& n_tiles, int& n_co, i
   a.ksplit = 1;
   a.csplit = a.C_in;
   const long long tiles = (long long)n_tiles * n_co * nz;
-  const int BK = 8;
-  if (tiles < 256 && a.C_in >= 4 * BK) {
-    int ks = (int)std::min<long long>((512 + tiles - 1) / tiles, (a.C_in + BK - 1) / BK);
+  const int BK = 8, min_ch = 4 * BK;
+  if (tiles < 256 && a.C_in >= 2 * min_ch) {
+    int ks = (int)std::min<long long>((512 + tiles - 1) / tiles, a.C_in / min_ch);
     int cs = ((a.C_in + ks - 1) / ks + BK - 1) / BK * BK;
     ks = (a.C_in + cs - 1) / cs;
     if (ks > 1) {
@@ -340,10 +355,16 @@ void launch_conv2d(const Conv2dLaunch& a0, hipStream_t st) {
     run_conv2d<32, 64, 32, 16, 8, 2>(a, n_tiles, n_co, nz, st);
   else if (c.BM == 16)
     run_conv2d<16, 256, 16, 64, 8, 1>(a, n_tiles, n_co, nz, st);
-  else if (c.BM == 32)
-    run_conv2d<32, 128, 32, 32, 8, 1>(a, n_tiles, n_co, nz, st);
-  else
+  else if (c.BM == 64 && c.BN == 128)
     run_conv2d<64, 128, 32, 64, 8, 1>(a, n_tiles, n_co, nz, st);
+  else if (c.BM == 32 && c.BN == 128)
+    run_conv2d<32, 128, 32, 32, 8, 1>(a, n_tiles, n_co, nz, st);
+  else if (c.BM == 64 && c.BN == 64)
+    run_conv2d<64, 64, 32, 32, 8, 1>(a, n_tiles, n_co, nz, st);
+  else if (c.BN == 64)
+    run_conv2d<32, 64, 16, 32, 8, 1>(a, n_tiles, n_co, nz, st);
+  else
+    run_conv2d<32, 32, 16, 16, 8, 1>(a, n_tiles, n_co, nz, st);
   if (a.ksplit > 1) {
     const long long total = (long long)nz * a.C_out * a.OH * a.OW;
     hipLaunchKernelGGL(conv2d_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a);
@@ -484,37 +505,40 @@ void launch_logmel_image(const float* M, int F, int Fp, int n_mels, float bn_s, 
 // Each direction runs on kGruGroups workgroups of four waves; wave w of group
 // g owns units 16 g + 4 w .. +3 and keeps their 12 rows of W_hh in registers
 // (lane l: columns 4 l .. 4 l + 3), so the recurrence reads no weights from
-// memory.  Per step every workgroup reads h_{t-1} (agent-coherent loads),
-// reduces its 12 dot products across the wave, updates its units, publishes
-// them to the other half of a double buffer and arrives at a per-direction
-// counter; the next step starts once all kGruGroups arrivals of this step
-// are visible.  The wait is bounded: past spin_limit polls (or once another
-// workgroup has given up) the workgroup sets the error flag and returns, so
-// the grid always drains; the host reports the flag.
+// memory.  The waves exchange h through a double buffer of 64-bit words
+// (step tag << 32 | float bits), written and read with agent-scope relaxed
+// atomics: step s waits until all H words of buffer (s-1)&1 carry tag s-1,
+// computes its 4 units and stores them, tagged s, into buffer s&1.  A value
+// and its step travel in one single-copy-atomic word, so no fence, counter or
+// barrier orders anything; the parity buffers keep a fast wave from
+// overwriting a word a slow wave has yet to read (it can only write step s
+// after every wave published step s-1, i.e. finished reading step s-2).
+// The wait is bounded: past spin_limit polls (or once another wave has given
+// up) the wave sets the error flag and returns, so the grid always drains;
+// the host reports the flag.
 namespace {
 constexpr int kGruGroups = 16;
 constexpr int kGruUnits = 16;  // per workgroup
 
-__device__ __forceinline__ float ld_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ unsigned long long gru_word(int tag, float v) {
+  return ((unsigned long long)(unsigned)tag << 32) | (unsigned long long)__float_as_uint(v);
 }
 
-__global__ void gru_init_kernel(float* state, unsigned* sync) {
-  const int i = threadIdx.x;
-  for (int k = i; k < 2 * 2 * 256; k += blockDim.x) state[k] = 0.f;
-  if (i < 4) sync[i] = 0u;
+__global__ void gru_init_kernel(unsigned long long* state, unsigned* sync) {
+  // buffer 1 holds h_{-1} = 0 tagged -1; buffer 0 a tag no step waits for
+  for (int k = threadIdx.x; k < 2 * 2 * 256; k += blockDim.x) state[k] = gru_word(((k >> 8) & 1) ? -1 : -2, 0.f);
+  if (threadIdx.x < 4) sync[threadIdx.x] = 0u;
 }
 
 __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
 #pragma clang fp contract(off)
-  __shared__ int go;
   const int d = blockIdx.x / kGruGroups;
   const int gw = blockIdx.x - d * kGruGroups;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int H = g.H;
   const int ub = gw * kGruUnits + wave * 4;
+  if (ub >= H) return;  // wave-uniform; no workgroup barrier below
   const float* W = g.whh + (long long)d * 3 * H * H;
   float wr[12][4];
 #pragma unroll
@@ -526,28 +550,59 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
         const int j = ub + u, col = 4 * lane + c;
         wr[q * 4 + u][c] = (j < H && col < H) ? W[(long long)(q * H + j) * H + col] : 0.f;
       }
-  const int ju = ub + (lane & 3);
+  const int u = lane & 3;
+  const int ju = ub + u;
   const bool owner = lane < 4 && ju < H;
   float bh[3];
 #pragma unroll
   for (int q = 0; q < 3; ++q) bh[q] = owner ? g.bhh[(long long)d * 3 * H + q * H + ju] : 0.f;
-  unsigned* cnt = g.sync + d;
+  unsigned long long* st = g.state + d * 2 * 256;
   unsigned* err = g.sync + 2;
 
   for (int s = 0; s < g.T; ++s) {
     const int t = d == 0 ? s : g.T - 1 - s;
-    const float* hp = g.state + (d * 2 + (s & 1)) * 256;
-    float hv[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) hv[c] = 4 * lane + c < H ? ld_agent(hp + 4 * lane + c) : 0.f;
-    float gxr = 0.f, gxz = 0.f, gxn = 0.f, hj = 0.f;
+    // gate inputs of this step: issued before the wait
+    float gxr = 0.f, gxz = 0.f, gxn = 0.f;
     if (owner) {
       const float* gp = g.gx + d * g.g_d + (long long)t * g.g_t;
       gxr = gp[(long long)ju * g.g_r];
       gxz = gp[(long long)(H + ju) * g.g_r];
       gxn = gp[(long long)(2 * H + ju) * g.g_r];
-      hj = ld_agent(hp + ju);
     }
+    // wait for h_{s-1}: all H words of buffer (s-1)&1 tagged s-1
+    const unsigned long long* hb = st + ((s - 1) & 1) * 256;
+    const unsigned want = (unsigned)(s - 1);
+    unsigned long long wv[4];
+    bool ready = true;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int col = 4 * lane + c;
+      wv[c] = col < H ? __hip_atomic_load(hb + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : gru_word(want, 0.f);
+      ready = ready && (unsigned)(wv[c] >> 32) == want;
+    }
+    long long polls = 0;
+    while (!__all(ready)) {
+      if (++polls > g.spin_limit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      ready = true;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = 4 * lane + c;
+        if (col < H && (unsigned)(wv[c] >> 32) != want)
+          wv[c] = __hip_atomic_load(hb + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ready = ready && (col >= H || (unsigned)(wv[c] >> 32) == want);
+      }
+    }
+    float hv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) hv[c] = __uint_as_float((unsigned)wv[c]);
+    // h_{s-1} of this lane's unit (word ju = ub + u sits in lane ub/4, element u)
+    const int src = ub >> 2;
+    const float h0 = __shfl(hv[0], src), h1 = __shfl(hv[1], src), h2 = __shfl(hv[2], src), h3 = __shfl(hv[3], src);
+    const float hj = u == 0 ? h0 : u == 1 ? h1 : u == 2 ? h2 : h3;
     float p[12];
 #pragma unroll
     for (int i = 0; i < 12; ++i) p[i] = ((wr[i][0] * hv[0] + wr[i][1] * hv[1]) + wr[i][2] * hv[2]) + wr[i][3] * hv[3];
@@ -556,7 +611,6 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
 #pragma unroll
       for (int i = 0; i < 12; ++i) p[i] += __shfl_xor(p[i], off);
     if (owner) {
-      const int u = lane & 3;
       const float sr = u == 0 ? p[0] : u == 1 ? p[1] : u == 2 ? p[2] : p[3];
       const float sz = u == 0 ? p[4] : u == 1 ? p[5] : u == 2 ? p[6] : p[7];
       const float sn = u == 0 ? p[8] : u == 1 ? p[9] : u == 2 ? p[10] : p[11];
@@ -564,30 +618,9 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
       const float zz = sigmoid_as(gxz + (sz + bh[1]));
       const float nn = tanhf(gxn + r * (sn + bh[2]));
       const float h = (1.0f - zz) * nn + zz * hj;
-      __hip_atomic_store(g.state + (d * 2 + ((s + 1) & 1)) * 256 + ju, h, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(st + (s & 1) * 256 + ju, gru_word(s, h), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       g.out[d * g.o_d + (long long)t * g.o_t + (long long)ju * g.o_j] = h;
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      const unsigned target = (unsigned)kGruGroups * (unsigned)(s + 1);
-      long long polls = 0;
-      int ok = 1;
-      while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-        if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u || ++polls > g.spin_limit) {
-          __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      go = ok;
-    }
-    __syncthreads();
-    if (!go) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
 }
 }  // namespace

@@ -6,11 +6,13 @@ per kernel launch shape, for the roofline figures of this backend.
 serves several decoder stages and the ConvTranspose phases, so the per-symbol
 average mixes shapes.  This groups dispatches by (symbol, grid, workgroup)
 instead, and reports the decoder ResBlock family the benchmark's roofline
-uses: every ``conv1d_mfma_kernel`` dispatch whose grid z is 3 (the three
-ResBlocks of a stage share one launch, z = 3 groups x batch 1) and whose grid
-is at least 64 workgroups wide (a ResBlock launch spans 10P..400P samples,
-at least 79 workgroups at P = 1000; the enc_p / flow convs span P samples, at
-most 32 workgroups, and their split-K launches can also have z = 3).
+uses: every persistent ``conv1d_mfma_persist_kernel<..., 1>`` dispatch (the
+instantiation reserved for launches of three stored groups: the three
+ResBlocks of a stage share one launch) and every one-shot
+``conv1d_mfma_kernel`` dispatch whose grid z is 3 and whose grid is at least
+64 workgroups wide (a ResBlock launch spans 10P..400P samples, at least 79
+workgroups at P = 1000; the enc_p / flow convs span P samples, at most 32
+workgroups, and their split-K launches can also have z = 3).
 
     python -m rvc_hip.profsum gpurun_out/prof/bench_results.db [--steps N]
 
@@ -71,6 +73,8 @@ def pmc_rows(db: str):
 
 
 def is_resblock(kernel: str, grid) -> bool:
+    if kernel.startswith("conv1d_mfma_persist_kernel"):
+        return kernel.replace(" ", "").endswith(",1>")   # FAM = 1: the three-group stored launches
     return kernel.startswith("conv1d_mfma_kernel") and grid[2] == 3 and grid[0] >= 64
 
 
@@ -108,7 +112,7 @@ def traffic(fetch_db: str, write_db: str, copy_fetch: str, copy_write: str, mib:
             fam_b += (rd + wr) * n
             fam_n += n
     if fam_n:
-        print(f"\nResBlock family (conv1d_mfma_kernel, grid z = 3, >= 64 wide): {fam_n} dispatches")
+        print(f"\nResBlock family (persistent FAM 1, or one-shot grid z = 3 and >= 64 wide): {fam_n} dispatches")
         print(f"resblock_traffic_bytes_per_launch: {int(round(fam_b / fam_n))}")
     return 0
 
@@ -145,7 +149,7 @@ def main(argv=None):
     n = sum(r["calls"] for r in rb)
     tot = sum(r["total_ms"] for r in rb)
     if n:
-        print(f"\nResBlock family (conv1d_mfma_kernel, grid z = 3, >= 64 wide): {n} dispatches, "
+        print(f"\nResBlock family (persistent FAM 1, or one-shot grid z = 3 and >= 64 wide): {n} dispatches, "
               f"{tot:.2f} ms total, average {tot * 1e3 / n:.1f} us per dispatch")
     allk = sum(r["total_ms"] for r in rows)
     print(f"all kernels: {allk:.2f} ms" + (f", {allk / args.steps:.3f} ms per step" if args.steps else ""))

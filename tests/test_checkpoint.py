@@ -154,3 +154,17 @@ def test_rejects_non_checkpoints(tmp_path):
                 zf.writestr(n, src.read(n))
     with pytest.raises(ck.CheckpointError, match="missing"):
         ck.load_pth(out.getvalue())
+
+
+def test_rmvpe_state_dict(tmp_path):
+    """rmvpe.pt layout: fp16 tensors plus BatchNorm num_batches_tracked
+    counters; the loader returns float32 arrays and drops the counters."""
+    w = syn.make_rmvpe_weights(seed=2)
+    keys = [k for k in w if k.startswith("unet.encoder.layers.0.") or k.startswith("fc.")]
+    sd = collections.OrderedDict((k, torch.from_numpy(np.ascontiguousarray(w[k])).half()) for k in keys)
+    sd["unet.encoder.bn.num_batches_tracked"] = torch.tensor(7)
+    out = ck.rmvpe_state_dict(ck.load_pth(_save(sd, tmp_path / "rmvpe.pt")))
+    assert set(out) == set(keys)
+    for k in keys:
+        assert out[k].dtype == np.float32
+        np.testing.assert_array_equal(out[k], w[k].astype(np.float16).astype(np.float32))

@@ -52,3 +52,18 @@ def test_hubert_from_pytorch_model_bin(tmp_path):
     np.testing.assert_array_equal(a.encode(x), b.encode(x))
     a.close()
     b.close()
+
+
+def test_rmvpe_from_pt(tmp_path):
+    from rvc_hip import checkpoint, synthetic as syn
+    from rvc_hip.rmvpe import HipRMVPE
+
+    w = syn.make_rmvpe_weights(seed=4)
+    sd = collections.OrderedDict((k, torch.from_numpy(np.ascontiguousarray(v)).half()) for k, v in w.items())
+    torch.save(sd, tmp_path / "rmvpe.pt")
+    a = checkpoint.load_rmvpe(tmp_path / "rmvpe.pt")
+    b = HipRMVPE({k: v.astype(np.float16).astype(np.float32) for k, v in w.items()})
+    x = syn.make_rmvpe_audio(6000, seed=1)
+    np.testing.assert_array_equal(a.infer_from_audio(x), b.infer_from_audio(x))
+    a.close()
+    b.close()
