@@ -276,22 +276,25 @@ long long conv2d_tiles(const Conv2dLaunch& a, const Conv2dCfg& c) {
          a.B;
 }
 
-// Largest tile whose grid still gives every CU a workgroup (256 CUs); the
-// 16-row tile for 16 output channels.  When even 32 x 32 tiles leave CUs
-// idle, the channels are split over workgroups (conv2d_plan).
+// Largest tile whose grid gives every CU about four workgroups (256 CUs):
+// each launch is short (0.6 GFLOP per U-Net conv at 10 s), so resident
+// workgroups hide one another's load latency; 16-row tiles for 16 output
+// channels.  When even 32 x 32 tiles leave CUs idle, the channels are split
+// over workgroups (conv2d_plan).
+constexpr long long kConv2dWant = 1024;
 Conv2dCfg conv2d_cfg(const Conv2dLaunch& a) {
   if (a.stride == 2) return {32, 64};
-  if (a.C_out <= 16) return {16, 256};
+  if (a.C_out <= 16) return conv2d_tiles(a, {16, 256}) >= kConv2dWant ? Conv2dCfg{16, 256} : Conv2dCfg{16, 128};
   static const Conv2dCfg order[] = {{64, 128}, {32, 128}, {64, 64}, {32, 64}, {32, 32}};
   for (const Conv2dCfg& c : order) {
     if (c.BM == 64 && a.C_out <= 32) continue;
-    if (conv2d_tiles(a, c) >= 256) return c;
+    if (conv2d_tiles(a, c) >= kConv2dWant) return c;
   }
   return {32, 32};
 }
 
 // channel split over workgroups when the tile grid cannot fill the GPU:
-// about 512 workgroups, at least 4 chunks of 8 channels per split
+// about kConv2dWant workgroups, at least 4 chunks of 8 channels per split
 void conv2d_plan(Conv2dLaunch& a, const Conv2dCfg& c, int& n_tiles, int& n_co, int& nz) {
   a.tile_c = std::min(c.BN, pow2_at_least(a.OW));
   const int TR = c.BN / a.tile_c;
@@ -303,7 +306,7 @@ void conv2d_plan(Conv2dLaunch& a, const Conv2dCfg& c, int& n_tiles, int& n_co, i
   const long long tiles = (long long)n_tiles * n_co * nz;
   const int BK = 8, min_ch = 4 * BK;
   if (tiles < 256 && a.C_in >= 2 * min_ch) {
-    int ks = (int)std::min<long long>((512 + tiles - 1) / tiles, a.C_in / min_ch);
+    int ks = (int)std::min<long long>((kConv2dWant + tiles - 1) / tiles, a.C_in / min_ch);
     int cs = ((a.C_in + ks - 1) / ks + BK - 1) / BK * BK;
     ks = (a.C_in + cs - 1) / cs;
     if (ks > 1) {
@@ -353,8 +356,10 @@ void launch_conv2d(const Conv2dLaunch& a0, hipStream_t st) {
   }
   if (a.stride == 2)
     run_conv2d<32, 64, 32, 16, 8, 2>(a, n_tiles, n_co, nz, st);
-  else if (c.BM == 16)
+  else if (c.BM == 16 && c.BN == 256)
     run_conv2d<16, 256, 16, 64, 8, 1>(a, n_tiles, n_co, nz, st);
+  else if (c.BM == 16)
+    run_conv2d<16, 128, 16, 32, 8, 1>(a, n_tiles, n_co, nz, st);
   else if (c.BM == 64 && c.BN == 128)
     run_conv2d<64, 128, 32, 64, 8, 1>(a, n_tiles, n_co, nz, st);
   else if (c.BM == 32 && c.BN == 128)

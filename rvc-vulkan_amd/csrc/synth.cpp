@@ -407,6 +407,9 @@ struct Synth : SessionBase {
   // conv (into dN<i>) and cv = cond(g). Ordered after everything already on
   // the engine stream; decode_main() waits for it.
   void decode_prep(const float* g, const float* f0, const float* ns, int B, int P) {
+    // a call that threw between its fork and its join leaves side-stream
+    // work behind; finish it before any of its buffers can be reallocated
+    if (side) RVC_HIP(hipStreamSynchronize(side));
     if (!side) {
       RVC_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
       RVC_HIP(hipEventCreateWithFlags(&forked, hipEventDisableTiming));
