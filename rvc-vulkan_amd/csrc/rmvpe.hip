@@ -84,15 +84,25 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv2d_mfma_kernel
   const int l16 = lane & 15;
 
   // staging map (fixed across chunks): input element e -> channel row and
-  // offset within that channel's plane (-1: outside the image / window)
+  // offset within that channel's plane (-1: outside the image / window).
+  // The quotients by the runtime plane / row widths come from a float
+  // reciprocal and one correction step (exact: operands < 2^24).
   const int nx = BK * plane;
+  const float inv_plane = 1.0f / (float)plane;
+  const float inv_wc = 1.0f / (float)WC;
+  auto qdiv = [](int n, int d, float inv) {
+    int q = (int)((float)n * inv);
+    if (q * d > n) --q;
+    else if ((q + 1) * d <= n) ++q;
+    return q;
+  };
   int xo[XPT], xr[XPT];
 #pragma unroll
   for (int e = 0; e < XPT; ++e) {
     const int idx = tid + e * NT;
-    const int r = idx / plane;
+    const int r = qdiv(idx, plane, inv_plane);
     const int rem = idx - r * plane;
-    const int rr = rem / WC;
+    const int rr = qdiv(rem, WC, inv_wc);
     const int cc = rem - rr * WC;
     const int h = h_lo + rr;
     const int w = w_lo + cc;
@@ -144,13 +154,15 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv2d_mfma_kernel
 #pragma unroll
     for (int n = 0; n < TN; ++n) acc[m][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // LDS offset of the window corner each of this lane's points reads
+  // LDS offset of the window corner each of this lane's points reads (TC is
+  // a power of two)
+  const int tcs = __builtin_ctz(TC);
   int pb[TN];
 #pragma unroll
   for (int n = 0; n < TN; ++n) {
     const int pn = wn * WN + n * 16 + l16;
-    const int pr = pn / TC;
-    const int pc = pn - pr * TC;
+    const int pr = pn >> tcs;
+    const int pc = pn & (TC - 1);
     pb[n] = pr * S * WC + pc * S;
   }
 
@@ -194,8 +206,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv2d_mfma_kernel
 #pragma unroll
     for (int n = 0; n < TN; ++n) {
       const int pn = wn * WN + n * 16 + l16;
-      const int pa = a0 + pn / TC;
-      const int pw = b0 + pn % TC;
+      const int pa = a0 + (pn >> tcs);
+      const int pw = b0 + (pn & (TC - 1));
       if (pa >= a.OH || pw >= a.OW) continue;
       const bool taps = pa < G.a_lim && pw < G.b_lim;
       const long long o = (long long)(pa * a.osh + G.oh0) * a.ors + (long long)(pw * a.osw + G.ow0) * a.ocs;

@@ -14,7 +14,7 @@ ResBlocks of a stage share one launch) and every one-shot
 workgroups at P = 1000; the enc_p / flow convs span P samples, at most 32
 workgroups, and their split-K launches can also have z = 3).
 
-    python -m rvc_hip.profsum gpurun_out/prof/bench_results.db [--steps N]
+    python -m rvc_hip.profsum prof/bench_results.db [--steps N]
 
 With ``--pmc`` it also reports the ``FETCH_SIZE`` / ``WRITE_SIZE`` counter
 means (KiB per dispatch) of a ``rocprofv3 --pmc`` database, grouped the same
