@@ -678,6 +678,60 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(ConvLaunch a) {
   *o = v;
 }
 
+// The WaveNet gate of the flow's coupling layers (runtime/models/vits.py:
+// 1086-1145) on the split-K sums of the in-layer conv: one thread per (b, c < H, t)
+// adds both halves' splits in order, then tanh(a + g_c) * sigmoid(b + g_{H+c})
+// in the expression order of the unfused path.
+__global__ __launch_bounds__(256) void splitk_reduce_gate_kernel(ConvLaunch a) {
+  const ConvGroup& G = a.g[0];
+  const int H = a.post_H, L = G.n_out;
+  const long long nfull = (long long)a.B * a.C_out * L;
+  const long long n = (long long)a.B * H * L;
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int t = (int)(e % L);
+  const int c = (int)((e / L) % H);
+  const int b = (int)(e / ((long long)L * H));
+  const long long e1 = ((long long)b * a.C_out + c) * L + t;
+  const long long e2 = e1 + (long long)H * L;
+  float v1 = a.part[e1], v2 = a.part[e2];
+  for (int s = 1; s < a.ksplit; ++s) {
+    v1 = v1 + a.part[e1 + (long long)s * nfull];
+    v2 = v2 + a.part[e2 + (long long)s * nfull];
+  }
+  if (G.bias) {
+    v1 = v1 + G.bias[c];
+    v2 = v2 + G.bias[H + c];
+  }
+  const float* g = a.post_g + (long long)b * a.post_gb;
+  G.out[(long long)b * a.ob + (long long)c * a.oc + t] = tanhf(v1 + g[c]) * sigmoid_as(v2 + g[H + c]);
+}
+
+// The residual / skip update of a WaveNet layer on the split-K sums of its
+// res-skip conv: h[c] += v_c for c < H (not the last layer), the skip
+// channels (all of them in the last layer) into skip (= in the first layer).
+__global__ __launch_bounds__(256) void splitk_reduce_update_kernel(ConvLaunch a) {
+  const ConvGroup& G = a.g[0];
+  const int H = a.post_H, L = G.n_out;
+  const long long n = (long long)a.B * a.C_out * L;
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int t = (int)(e % L);
+  const int co = (int)((e / L) % a.C_out);
+  const int b = (int)(e / ((long long)L * a.C_out));
+  float v = a.part[e];
+  for (int s = 1; s < a.ksplit; ++s) v = v + a.part[e + (long long)s * n];
+  if (G.bias) v = v + G.bias[co];
+  const long long hb = ((long long)b * H) * L + t;
+  if (!a.post_last && co < H) {
+    float* p = a.post_h + hb + (long long)co * L;
+    *p = *p + v;
+  } else {
+    float* p = a.post_skip + hb + (long long)(a.post_last ? co : co - H) * L;
+    *p = a.post_first ? v : *p + v;
+  }
+}
+
 constexpr size_t kLdsLimit = 65536;
 
 int max_n_out(const ConvLaunch& a) {
@@ -834,7 +888,14 @@ long long n_blocks(const ConvLaunch& a, int BM, int BN) {
 void launch_splitk_reduce(const ConvLaunch& a, hipStream_t s) {
   const long long n = (long long)a.B * a.C_out * a.g[0].n_out;
   if (n <= 0) return;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  if (a.post == POST_WN_GATE) {
+    const long long ng = (long long)a.B * a.post_H * a.g[0].n_out;
+    hipLaunchKernelGGL(splitk_reduce_gate_kernel, dim3((unsigned)((ng + 255) / 256)), dim3(256), 0, s, a);
+  } else if (a.post == POST_WN_UPDATE) {
+    hipLaunchKernelGGL(splitk_reduce_update_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  }
   check_launch("splitk_reduce");
 }
 
@@ -853,6 +914,7 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
             "conv1d_mfma: invalid shape");
   const int step = a.g[0].in_step <= 1 ? 1 : a.g[0].in_step;
   RVC_CHECK(step == 1 || step == 2, "conv1d_mfma: input stride must be 1 or 2");
+  RVC_CHECK(a.post == POST_NONE || (a.n_groups == 1 && step == 1 && a.part), "conv1d_mfma: a reduce post-op needs the split-K path");
   for (int g = 0; g < a.n_groups; ++g) {
     RVC_CHECK(a.g[g].n_out >= 0 && conv1d_mfma_supported(a.g[g].K, a.g[g].dil),
               "conv1d_mfma: taps / dilation outside the MFMA path");
@@ -890,6 +952,7 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
       if (ok) return;
     }
   }
+  RVC_CHECK(a.post == POST_NONE, "conv1d_mfma: a reduce post-op needs the split-K path");
   int kmax = 0;
   for (int g = 0; g < a.n_groups; ++g) kmax = std::max(kmax, a.g[g].K);
   if (kmax == 1) {  // 1x1 convolutions: plain GEMMs with 32-channel chunks

@@ -118,7 +118,18 @@ struct ConvLaunch {
   float* part;
   size_t part_floats;
   int ksplit, csplit;  // set by the launcher
+  // what the split-K reduce does with v = sum of the splits + bias (the
+  // launch must take the split path: conv1d_mfma_split_floats(a) > 0):
+  //   POST_WN_GATE   (C_out = 2H): out[c][t] = tanh(v_c + g[c]) * sig(v_{H+c} + g[H+c])
+  //                  for c < H, out of row stride oc, g per batch item (stride post_gb)
+  //   POST_WN_UPDATE (C_out = 2H, or H when post_last): h += v_c (c < H, not last),
+  //                  skip = / += v of the skip channels (post_first: =)
+  int post;
+  const float* post_g; long long post_gb;
+  float* post_h; float* post_skip;
+  int post_H, post_first, post_last;
 };
+enum Post : int { POST_NONE = 0, POST_WN_GATE = 1, POST_WN_UPDATE = 2 };
 
 // MFMA implicit-GEMM conv1d (input stride 1 or 2, the same for every group
 // of a launch), K <= kConvTapsMax and (K-1)*dil <= kConvHaloMax.

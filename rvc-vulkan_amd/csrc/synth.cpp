@@ -387,11 +387,37 @@ struct Synth : SessionBase {
       conv("flow.pre", c1x1(dst, HP, L.pre_w, L.pre_b, h, B, half, H, P));
       launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s);
       for (int i = 0; i < kWnLayers; ++i) {
-        conv("flow.in", cargs_same(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
-                              (kWnKernel - 1) / 2));
-        launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
-        conv("flow.rs", c1x1(acts, HP, L.rs_w[i], L.rs_b[i], rs, B, H, L.rs_out[i], P));
-        launch_wn_update(h, skip, rs, B, H, P, i == 0, i == kWnLayers - 1, s);
+        // in-layer conv + gate, and res/skip conv + update: fused into the
+        // split-K reduce when the conv takes the split path (it does at
+        // P <= ~2000), as separate elementwise launches otherwise
+        ConvLaunch ci = cargs_same(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
+                                   (kWnKernel - 1) / 2);
+        if (conv1d_mfma_split_floats(ci) > 0) {
+          ci.post = POST_WN_GATE;
+          ci.post_g = gv + (long long)i * 2 * H;
+          ci.post_gb = (long long)2 * H * kWnLayers;
+          ci.post_H = H;
+          ci.g[0].out = acts;
+          ci.ob = HP;
+          ci.oc = P;
+          conv("flow.in", ci);
+        } else {
+          conv("flow.in", ci);
+          launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
+        }
+        ConvLaunch cr = c1x1(acts, HP, L.rs_w[i], L.rs_b[i], rs, B, H, L.rs_out[i], P);
+        if (conv1d_mfma_split_floats(cr) > 0) {
+          cr.post = POST_WN_UPDATE;
+          cr.post_h = h;
+          cr.post_skip = skip;
+          cr.post_H = H;
+          cr.post_first = i == 0;
+          cr.post_last = i == kWnLayers - 1;
+          conv("flow.rs", cr);
+        } else {
+          conv("flow.rs", cr);
+          launch_wn_update(h, skip, rs, B, H, P, i == 0, i == kWnLayers - 1, s);
+        }
       }
       conv("flow.post", c1x1(skip, HP, L.post_w, L.post_b, m, B, H, half, P));
       launch_sub_inplace_strided(dst + (long long)half * P, HP, m, (long long)half * P, B, half, P, s);
