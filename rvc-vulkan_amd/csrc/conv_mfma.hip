@@ -429,6 +429,16 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   int item = blockIdx.x;
   if (item >= n_items) return;  // uniform for the whole workgroup, before any barrier
   const int nchunk = a.C_in / BKT;  // the launcher requires C_in % BK == 0
+  // Item scheduling.  Static: slot s runs items s, s + grid, ...  Dynamic
+  // (a.queue): every workgroup starts on item blockIdx.x, then takes tickets
+  // from the queue of its XCD slot class x = blockIdx.x % 8 (items x + 8 m,
+  // heaviest group first), so a slot that drew light items takes more of
+  // them and the items of one column tile still meet on one XCD.
+  __shared__ int next_sh;
+  const bool dyn = a.queue != nullptr && n_items > (int)gridDim.x;
+  const int nq = gridDim.x % 8 == 0 ? 8 : 1;
+  const int qx = blockIdx.x % nq;
+  const int per_q = gridDim.x / nq;
 
   extern __shared__ float smem[];
   const int tid = threadIdx.x;
@@ -563,7 +573,19 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   lstore(0);
   __syncthreads();
   int buf = 0;
-  for (; item < n_items; item += gridDim.x) {
+  while (item < n_items) {
+    // this workgroup's next item: the ticket is drawn now and published to
+    // LDS behind the first chunk's MFMAs (its round trip overlaps them), read
+    // by every thread after that chunk's barrier
+    unsigned tk = 0;
+    if (tid == 0 && dyn) tk = atomicAdd(a.queue + qx, 1u);
+    auto publish = [&]() {
+      if (tid == 0) next_sh = dyn ? qx + nq * (per_q + (int)tk) : item + (int)gridDim.x;
+    };
+    if (nchunk == 1) {
+      publish();
+      __syncthreads();
+    }
     // the current item's geometry, kept before setup() moves on to the next
     const int c_gi = s_gi, c_b = s_b, c_i0 = s_i0, c_co0 = s_co0, c_K = s_K, c_dil = s_dil, c_XW = s_XW;
 #pragma unroll
@@ -579,14 +601,16 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
       gload((c + 1) * BKT);
       mfma_chunk(buf, c_K, c_dil, c_XW);
       lstore(buf ^ 1);
+      if (c == 0) publish();
       __syncthreads();
       buf ^= 1;
     }
     // the last chunk: prefetch the next item's first chunk and this item's
     // epilogue operand (the residual, or the current output for ADD)
-    const bool more = item + (int)gridDim.x < n_items;
+    const int next = next_sh;
+    const bool more = next < n_items;
     if (more) {
-      setup(item + gridDim.x);
+      setup(next);
       gload(0);
     }
     // Epilogue addressing through buffer resources over this batch item's
@@ -649,7 +673,12 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), ors, ooff[n], 4 * roff * (int)a.oc, 0);
         }
     }
+    item = next;
   }
+  // the last workgroup to finish (every other one has drawn its final ticket)
+  // clears the counters for the next launch on this buffer
+  if (dyn && tid == 0 && atomicAdd(a.queue + 8, 1u) == gridDim.x - 1)
+    for (int i = 0; i < 9; ++i) __hip_atomic_store(a.queue + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits

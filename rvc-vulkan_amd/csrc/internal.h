@@ -128,6 +128,10 @@ struct ConvLaunch {
   const float* post_g; long long post_gb;
   float* post_h; float* post_skip;
   int post_H, post_first, post_last;
+  // persistent launches: 9 zeroed counters (8 per-XCD item queues and a
+  // finish count, reset by the launch's last workgroup) for dynamic item
+  // scheduling; null: static round-robin.  One launch at a time per buffer.
+  unsigned* queue;
 };
 enum Post : int { POST_NONE = 0, POST_WN_GATE = 1, POST_WN_UPDATE = 2 };
 

@@ -114,6 +114,21 @@ struct SessionBase {
     return upload(t.data);
   }
 
+  // item-queue counters of this session's persistent conv launches (all on
+  // the engine stream, so one launch at a time uses them); zeroed once here,
+  // then reset by each launch's last workgroup
+  unsigned* pq = nullptr;
+  unsigned* persist_queue() {
+    if (!pq) {
+      void* p = nullptr;
+      RVC_HIP(hipMalloc(&p, 16 * sizeof(unsigned)));
+      owned.push_back(p);
+      RVC_HIP(hipMemsetAsync(p, 0, 16 * sizeof(unsigned), eng->stream));
+      pq = static_cast<unsigned*>(p);
+    }
+    return pq;
+  }
+
   // -------------------------------------------------------------- workspace
   float* buf(const std::string& name, size_t n) {
     auto it = ws.find(name);
@@ -230,6 +245,7 @@ struct SessionBase {
       sa.part = buf("splitk", need);
       sa.part_floats = need;
     }
+    if (!b16) sa.queue = persist_queue();
     run(t, 2.0 * mac, bytes, [&] {
       if (b16)
         launch_conv1d_bf16(sa, eng->stream);
