@@ -869,7 +869,7 @@ bool launch_persist(const ConvLaunch& a, hipStream_t s) {
 // Split-K plan for a single-group stride-1 launch whose output tiles alone
 // cannot fill the GPU: 128 x 128 (or 64 x 128) tiles and the input channels
 // cut into S splits of whole BKT-channel chunks (at least two chunks each),
-// so tiles x S reaches about 640 workgroups.  Depends on the per-item tile
+// so tiles x S reaches about 384 workgroups.  Depends on the per-item tile
 // count only, never on B, so batched calls keep the per-chunk results.
 long long n_blocks(const ConvLaunch& a, int BM, int BN);
 
@@ -893,7 +893,10 @@ SplitPlan split_plan(const ConvLaunch& a) {
   if (n_blocks(a, 64, 128) >= 384) return p;  // the tile grid alone fills the GPU
   const long long nb = n_blocks(a, BM, 128);
   const int max_s = a.C_in / (2 * BKT);
-  int S = (int)std::min<long long>((640 + nb - 1) / nb, max_s);
+  // about 384 workgroups: measured against 256 / 320 / 448 / 640 on the
+  // enc_p + flow convs (P = 1000) and HuBERT's 499-frame GEMMs, where more
+  // splits cost more in partial-sum traffic than they gain in parallelism
+  int S = (int)std::min<long long>((384 + nb - 1) / nb, max_s);
   if (S < 2) return p;
   const int chunks = (a.C_in + BKT - 1) / BKT;
   const int per = (chunks + S - 1) / S;
