@@ -194,21 +194,27 @@ int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
                    int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h, int64_t pad_w, int64_t stride_h,
                    int64_t stride_w);
 int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
+/* rvc_conv_t2d (ffi.zig:428, engine.zig:1511): out[B][C_out][h_out][w_out] =
+ * conv_transpose2d(x[B][C_in][ih][iw], w[C_in][C_out][kh][kw]), stride (sh, sw),
+ * padding (ph, pw), output padding < stride, no bias; h_out / w_out must match
+ * the transposed-conv formula; kh, kw <= 3 and sh, sw <= 2 on this backend.
+ * rvc_insert_zeros_2x (ffi.zig:481, engine.zig:1704): out[C][2H-1][2W-1] = x at
+ * even rows and columns, zeros elsewhere (RMVPE's zero-inserted ConvTranspose
+ * input, fed to rvc_conv2d). */
+int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, int64_t c_in, int64_t ih, int64_t iw,
+                     int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                     int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out);
+int32_t rvc_insert_zeros_2x(int64_t h, int64_t x, int64_t out, int64_t c, int64_t ih, int64_t iw);
 
 /* ---------------------------------------------------------------- not provided
  * Exported so the reference's loader (runtime/_vulkan.py:148-278 binds every
  * symbol) can load this library; each returns -1 with a message.  They serve
  * training and the reference's record/commit form of the RMVPE ops:
- * rvc_matmul_f16 (ffi.zig:246), rvc_conv_t2d (:428), rvc_insert_zeros_2x (:483),
- * rvc_batch_add_conv2d (:1196), rvc_batch_add_conv_t2d (:1246),
+ * rvc_matmul_f16 (ffi.zig:246), rvc_batch_add_conv2d (:1196), rvc_batch_add_conv_t2d (:1246),
  * rvc_batch_add_im2col_1d (:1304), rvc_batch_add_im2col_2d (:1341),
  * rvc_batch_add_gru (:1377), rvc_batch_add_gru_sync (:1411).  RMVPE as a whole
  * runs in the rvc_rmvpe_* session below. */
 int32_t rvc_matmul_f16(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
-int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, int64_t c_in, int64_t ih, int64_t iw,
-                     int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
-                     int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out);
-int32_t rvc_insert_zeros_2x(int64_t h, int64_t x, int64_t out, int64_t c, int64_t ih, int64_t iw);
 int32_t rvc_batch_add_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
                              int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h,
                              int64_t pad_w, int64_t stride_h, int64_t stride_w);

@@ -1133,6 +1133,8 @@ int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
       }
     g.a_lim = (int)OH;
     g.b_lim = (int)OW;
+    g.oh_n = (int)OH;
+    g.ow_n = (int)OW;
     a.x = xp; a.xb = c_in * H * W; a.xc = H * W; a.H = (int)H; a.W = (int)W;
     a.out = op; a.ob = c_out * OH * OW; a.oc = OH * OW; a.ors = OW; a.ocs = 1;
     a.bias = bp; a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
@@ -1151,12 +1153,103 @@ int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
     });
   });
 }
-int32_t rvc_conv_t2d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                     int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
-  return not_provided("rvc_conv_t2d");
+// engine/src/ffi.zig:428-479 + engine.zig:1511-1560: out[B][C_out][h_out][w_out]
+// = conv_transpose2d(x[B][C_in][ih][iw], w[C_in][C_out][kh][kw]), stride (sh, sw),
+// padding (ph, pw), output padding (opad_h, opad_w) < stride, no bias.  Output
+// row o = c + sh*a of stride phase c takes the taps k = c + ph (mod sh) of input
+// row a + (c + ph - k) / sh (columns alike); every phase is one group of the
+// conv2d MFMA kernel with its own extent.  Kernels up to 3x3 and strides up to
+// 2 on this backend.
+int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, int64_t c_in, int64_t ih, int64_t iw,
+                     int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                     int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out) {
+  return guarded(h, [&](Engine& e) {
+    RVC_CHECK(B >= 1 && c_in >= 1 && ih >= 1 && iw >= 1 && c_out >= 1 && kh >= 1 && kw >= 1 && sh >= 1 && sw >= 1 &&
+                  ph >= 0 && pw >= 0 && opad_h >= 0 && opad_w >= 0,
+              "conv_t2d: invalid dimensions");
+    RVC_CHECK(opad_h < sh && opad_w < sw, "conv_t2d: output padding must be smaller than the stride");
+    const long long hext = (ih - 1) * sh + (kh - 1), wext = (iw - 1) * sw + (kw - 1);
+    RVC_CHECK(2 * ph <= hext && 2 * pw <= wext, "conv_t2d: padding must fit the upsampled extent");
+    RVC_CHECK(h_out == hext + opad_h + 1 - 2 * ph && w_out == wext + opad_w + 1 - 2 * pw,
+              "conv_t2d: h_out / w_out do not match the transposed-conv formula");
+    RVC_CHECK(kh <= 3 && kw <= 3 && sh <= 2 && sw <= 2, "conv_t2d: this backend takes kernels up to 3x3 and strides up to 2");
+    RVC_CHECK(B * c_in * ih * iw < (1LL << 40) && c_in <= (1 << 20) && c_out <= (1 << 20) && h_out * w_out < (1LL << 31),
+              "conv_t2d: too large");
+    const float* xp = e.fptr(x, B * c_in * ih * iw, "conv_t2d x");
+    const float* wp = e.fptr(w, c_in * c_out * kh * kw, "conv_t2d w");
+    float* op = e.fptr(out, B * c_out * h_out * w_out, "conv_t2d out");
+    Conv2dLaunch a{};
+    ConvT2dTaps taps[kConv2dGroupsMax];
+    int maxh = 0, maxw = 0;
+    for (int c = 0; c < sh; ++c)
+      for (int d = 0; d < sw; ++d) {
+        const int oh_n = c < h_out ? (int)((h_out - c + sh - 1) / sh) : 0;
+        const int ow_n = d < w_out ? (int)((w_out - d + sw - 1) / sw) : 0;
+        if (oh_n == 0 || ow_n == 0) continue;
+        Conv2dGroup& g = a.g[a.n_groups];
+        ConvT2dTaps& t = taps[a.n_groups];
+        t.n = 0;
+        for (int i = 0; i < kh; ++i) {
+          if ((c + ph - i) % sh != 0) continue;
+          for (int j = 0; j < kw; ++j) {
+            if ((d + pw - j) % sw != 0) continue;
+            t.kh[t.n] = i;
+            t.kw[t.n] = j;
+            g.dh[t.n] = (int)((c + ph - i) / sh);
+            g.dw[t.n] = (int)((d + pw - j) / sw);
+            ++t.n;
+          }
+        }
+        if (t.n == 0) {  // no tap reaches this phase: zeros
+          t.n = 1;
+          t.kh[0] = t.kw[0] = -1;
+          g.dh[0] = g.dw[0] = 0;
+        }
+        g.ntaps = t.n;
+        g.oh0 = c;
+        g.ow0 = d;
+        g.a_lim = g.oh_n = oh_n;
+        g.b_lim = g.ow_n = ow_n;
+        maxh = std::max(maxh, oh_n);
+        maxw = std::max(maxw, ow_n);
+        ++a.n_groups;
+      }
+    a.x = xp; a.xb = c_in * ih * iw; a.xc = ih * iw; a.H = (int)ih; a.W = (int)iw;
+    a.out = op; a.ob = c_out * h_out * w_out; a.oc = h_out * w_out; a.ors = w_out; a.ocs = 1;
+    a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
+    a.OH = maxh; a.OW = maxw; a.osh = (int)sh; a.osw = (int)sw; a.stride = 1;
+    size_t wfl = 0;
+    for (int gi = 0; gi < a.n_groups; ++gi) wfl += (size_t)taps[gi].n * c_in * a.w_ld;
+    const size_t need = conv2d_split_floats(a);
+    float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (wfl + need)));
+    size_t off = 0;
+    for (int gi = 0; gi < a.n_groups; ++gi) {
+      a.g[gi].w = sc + off;
+      off += (size_t)taps[gi].n * c_in * a.w_ld;
+    }
+    if (need > 0) {
+      a.part = sc + wfl;
+      a.part_floats = need;
+    }
+    submit(e, [&] {
+      for (int gi = 0; gi < a.n_groups; ++gi)
+        launch_pack_convt2d_phase(wp, const_cast<float*>(a.g[gi].w), (int)c_in, (int)c_out, (int)kh, (int)kw, taps[gi],
+                                  e.stream);
+      launch_conv2d(a, e.stream);
+    });
+  });
 }
-int32_t rvc_insert_zeros_2x(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
-  return not_provided("rvc_insert_zeros_2x");
+
+// engine/src/ffi.zig:481-496 + engine.zig:1704-1722: out[C][2H-1][2W-1] holds
+// x[C][H][W] at even rows and columns, zeros elsewhere (C = batch x channels).
+int32_t rvc_insert_zeros_2x(int64_t h, int64_t x, int64_t out, int64_t c, int64_t h_, int64_t w) {
+  return guarded(h, [&](Engine& e) {
+    RVC_CHECK(c >= 1 && h_ >= 1 && w >= 1, "insert_zeros_2x: invalid dimensions");
+    RVC_CHECK(c * (2 * h_ - 1) * (2 * w - 1) < (1LL << 40) && h_ < (1 << 30) && w < (1 << 30), "insert_zeros_2x: too large");
+    const float* xp = e.fptr(x, c * h_ * w, "insert_zeros_2x x");
+    float* op = e.fptr(out, c * (2 * h_ - 1) * (2 * w - 1), "insert_zeros_2x out");
+    submit(e, [&] { launch_insert_zeros_2x(xp, op, c, (int)h_, (int)w, e.stream); });
+  });
 }
 int32_t rvc_batch_add_conv2d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                              int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {

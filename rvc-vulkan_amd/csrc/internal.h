@@ -324,7 +324,7 @@ void launch_matmul(const float* a, const float* b, float* c, int M, int K, int N
 
 // ------------------------------------------------------------------ conv2d
 // Implicit-GEMM 2-D convolution on fp32 MFMA (csrc/rmvpe.hip).  Computed
-// point (a, b) of group g (a < OH, b < OW) sums, over taps t and input
+// point (a, b) of group g (a < oh_n <= OH, b < ow_n <= OW) sums, over taps t and input
 // channels ci, w_t[ci][co] * x[ci][a*stride + dh_t][b*stride + dw_t] (zero
 // outside [0, H) x [0, W)); points with a >= a_lim or b >= b_lim take no taps.
 // v = acc + bias; relu; + res; stored at
@@ -337,6 +337,7 @@ struct Conv2dGroup {
   int dh[kConv2dTapsMax], dw[kConv2dTapsMax];
   int oh0, ow0;
   int a_lim, b_lim;
+  int oh_n, ow_n;  // this group's computed extent (<= OH, OW); points beyond it are not stored
   int dh_lo, dw_lo, dh_span, dw_span;  // set by the launcher
 };
 struct Conv2dLaunch {
@@ -359,6 +360,15 @@ void launch_conv2d(const Conv2dLaunch& a, hipStream_t s);
 // [KH*KW][C_in][packed_ld(C_out)], tap t = kh*KW + kw
 std::vector<float> pack_conv2d_host(const float* w, const float* scale, int C_out, int C_in, int KH, int KW);
 void launch_pack_conv2d_weight(const float* w, float* out, int C_out, int C_in, int KH, int KW, hipStream_t s);
+// ConvTranspose2d weights w [C_in][C_out][KH][KW] -> [ntaps][C_in][packed_ld(C_out)] for the taps (kh[t], kw[t])
+// of one stride phase (kh[t] < 0: an all-zero tap)
+struct ConvT2dTaps {
+  int n;
+  int kh[kConv2dTapsMax], kw[kConv2dTapsMax];
+};
+void launch_pack_convt2d_phase(const float* w, float* out, int C_in, int C_out, int KH, int KW, const ConvT2dTaps& t,
+                               hipStream_t s);
+void launch_insert_zeros_2x(const float* x, float* out, long long C, int H, int W, hipStream_t s);
 void launch_avg_pool2(const float* x, float* out, int BC, int H, int W, hipStream_t s);
 
 // ------------------------------------------------------------------ RMVPE

@@ -292,6 +292,8 @@ struct Rmvpe : SessionBase {
     g.oh0 = g.ow0 = 0;
     g.a_lim = H;
     g.b_lim = Wd;
+    g.oh_n = H;
+    g.ow_n = Wd;
     a.x = x; a.xb = (long long)ci * H * Wd; a.xc = (long long)H * Wd; a.H = H; a.W = Wd;
     a.out = out; a.ob = (long long)co * H * Wd; a.oc = (long long)H * Wd; a.ors = Wd; a.ocs = 1;
     a.res = res; a.bias = bias; a.relu = relu ? 1 : 0;
@@ -344,6 +346,8 @@ struct Rmvpe : SessionBase {
         // (symmetric padding + zero-filled output padding, rmvpe.py:369-383)
         g.a_lim = ph ? H - 1 : H;
         g.b_lim = pw ? Wd - 1 : Wd;
+        g.oh_n = H;
+        g.ow_n = Wd;
       }
     a.x = x; a.xb = (long long)u.ci * H * Wd; a.xc = (long long)H * Wd; a.H = H; a.W = Wd;
     a.out = out; a.ob = (long long)u.co * 4 * H * Wd; a.oc = 4LL * H * Wd; a.ors = 2 * Wd; a.ocs = 1;
@@ -443,6 +447,8 @@ struct Rmvpe : SessionBase {
       }
       g.a_lim = Fp;
       g.b_lim = kMels;
+      g.oh_n = Fp;
+      g.ow_n = kMels;
       a.x = cur; a.xb = (long long)en[0] * Fp * kMels; a.xc = (long long)Fp * kMels; a.H = Fp; a.W = kMels;
       // (c, h, w) -> row c*128 + w, column h: the reference's
       // transpose(0, 2, 1, 3).reshape(F', 384), channel-major for the GEMM

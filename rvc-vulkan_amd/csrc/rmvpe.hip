@@ -208,7 +208,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv2d_mfma_kernel
       const int pn = wn * WN + n * 16 + l16;
       const int pa = a0 + (pn >> tcs);
       const int pw = b0 + (pn & (TC - 1));
-      if (pa >= a.OH || pw >= a.OW) continue;
+      if (pa >= G.oh_n || pw >= G.ow_n) continue;
       const bool taps = pa < G.a_lim && pw < G.b_lim;
       const long long o = (long long)(pa * a.osh + G.oh0) * a.ors + (long long)(pw * a.osw + G.ow0) * a.ocs;
 #pragma unroll
@@ -245,6 +245,7 @@ __global__ __launch_bounds__(256) void conv2d_reduce_kernel(Conv2dLaunch a) {
   const int pa = (int)(p / a.OW);
   const int pw = (int)(p - (long long)pa * a.OW);
   const Conv2dGroup& G = a.g[gi];
+  if (pa >= G.oh_n || pw >= G.ow_n) return;
   const long long o = (long long)(pa * a.osh + G.oh0) * a.ors + (long long)(pw * a.osw + G.ow0) * a.ocs;
   float v = s;
   if (a.bias) v = v + a.bias[co];
@@ -357,6 +358,7 @@ void launch_conv2d(const Conv2dLaunch& a0, hipStream_t st) {
       wl = std::min(wl, G.dw[t]); wh = std::max(wh, G.dw[t]);
     }
     RVC_CHECK(hh - hl <= 2 && wh - wl <= 2, "conv2d: tap offsets must span at most 3 rows and 3 columns");
+    RVC_CHECK(G.oh_n >= 0 && G.oh_n <= a.OH && G.ow_n >= 0 && G.ow_n <= a.OW, "conv2d: group extent outside the grid");
     G.dh_lo = hl; G.dw_lo = wl; G.dh_span = hh - hl; G.dw_span = wh - wl;
   }
   const Conv2dCfg c = conv2d_cfg(a);
@@ -415,6 +417,30 @@ __global__ void pack_conv2d_kernel(const float* w, float* out, int C_out, int C_
   out[i] = co < C_out ? w[(((long long)co * C_in + ci) * KH + t / KW) * KW + t % KW] : 0.f;
 }
 
+__global__ void pack_convt2d_phase_kernel(const float* w, float* out, int C_in, int C_out, int KH, int KW, int ld,
+                                          ConvT2dTaps t) {
+  const long long n = (long long)t.n * C_in * ld;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int co = (int)(i % ld);
+  const long long r = i / ld;
+  const int ci = (int)(r % C_in);
+  const int k = (int)(r / C_in);
+  const int kh = t.kh[k], kw = t.kw[k];
+  out[i] = (co < C_out && kh >= 0) ? w[(((long long)ci * C_out + co) * KH + kh) * KW + kw] : 0.f;
+}
+
+__global__ void insert_zeros_2x_kernel(const float* x, float* out, long long n, int H, int W) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int UW = 2 * W - 1, UH = 2 * H - 1;
+  const int u = (int)(i % UW);
+  const long long r = i / UW;
+  const int v = (int)(r % UH);
+  const long long c = r / UH;
+  out[i] = ((u | v) & 1) ? 0.f : x[(c * H + (v >> 1)) * W + (u >> 1)];
+}
+
 __global__ void avg_pool2_kernel(const float* x, float* out, long long n, int H, int W) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -434,6 +460,22 @@ void launch_pack_conv2d_weight(const float* w, float* out, int C_out, int C_in, 
   hipLaunchKernelGGL(pack_conv2d_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w, out, C_out, C_in,
                      KH, KW, packed_ld(C_out));
   check_launch("pack_conv2d");
+}
+
+void launch_pack_convt2d_phase(const float* w, float* out, int C_in, int C_out, int KH, int KW, const ConvT2dTaps& t,
+                               hipStream_t s) {
+  RVC_CHECK(t.n >= 1 && t.n <= kConv2dTapsMax, "pack_convt2d: 1..9 taps");
+  const long long n = (long long)t.n * C_in * packed_ld(C_out);
+  hipLaunchKernelGGL(pack_convt2d_phase_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w, out, C_in,
+                     C_out, KH, KW, packed_ld(C_out), t);
+  check_launch("pack_convt2d_phase");
+}
+
+void launch_insert_zeros_2x(const float* x, float* out, long long C, int H, int W, hipStream_t s) {
+  const long long n = C * (2LL * H - 1) * (2LL * W - 1);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(insert_zeros_2x_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, out, n, H, W);
+  check_launch("insert_zeros_2x");
 }
 
 void launch_avg_pool2(const float* x, float* out, int BC, int H, int W, hipStream_t s) {

@@ -220,3 +220,70 @@ def test_rmvpe_timing_breakdown(hr):
     t = hr.timing()
     hr.set_timing("")
     assert t["launches"] > 100 and t["ms"] > 0 and t["flops"] > 1e9
+
+
+@pytest.mark.parametrize("B,C_in,ih,iw,C_out,kh,kw,sh,sw,ph,pw,oph,opw", [
+    (1, 8, 5, 7, 6, 3, 3, 2, 2, 1, 1, 1, 1),     # RMVPE's decoder shape
+    (2, 16, 4, 4, 8, 2, 2, 2, 2, 0, 0, 0, 0),
+    (1, 12, 6, 5, 10, 3, 3, 1, 1, 1, 1, 0, 0),
+    (1, 8, 5, 6, 4, 3, 2, 2, 1, 1, 0, 1, 0),     # different strides per axis
+    (1, 8, 4, 5, 8, 1, 1, 2, 2, 0, 0, 1, 1),     # phases no tap reaches: zeros
+    (1, 40, 9, 3, 24, 3, 3, 2, 2, 0, 1, 1, 0),
+])
+def test_conv_t2d_export_vs_torch(B, C_in, ih, iw, C_out, kh, kw, sh, sw, ph, pw, oph, opw):
+    import torch
+
+    from rvc_hip import _hip
+
+    ctx = _ctx()
+    L = _hip.get_lib()
+    rng = np.random.default_rng(C_in + kh * 10 + sh)
+    x = rng.standard_normal((B, C_in, ih, iw)).astype(np.float32)
+    w = (rng.standard_normal((C_in, C_out, kh, kw)) / np.sqrt(C_in * kh * kw)).astype(np.float32)
+    ref = torch.nn.functional.conv_transpose2d(torch.from_numpy(x), torch.from_numpy(w), stride=(sh, sw),
+                                               padding=(ph, pw), output_padding=(oph, opw)).numpy()
+    H, W = ref.shape[2], ref.shape[3]
+    ids = [ctx.upload(x), ctx.upload(w), ctx.alloc(B * C_out * H * W)]
+    try:
+        print(f"conv_t2d {x.shape} k{kh}x{kw} s{sh}x{sw} p{ph}x{pw} op{oph}x{opw}", flush=True)
+        _hip._check(L.rvc_conv_t2d(ctx.handle, ids[0], ids[1], ids[2], B, C_in, ih, iw, C_out, kh, kw, sh, sw, ph, pw,
+                                   oph, opw, H, W), "rvc_conv_t2d")
+        got = ctx.download(ids[2], ref.shape)
+        assert L.rvc_conv_t2d(ctx.handle, ids[0], ids[1], ids[2], B, C_in, ih, iw, C_out, kh, kw, sh, sw, ph, pw,
+                              oph, opw, H + 1, W) == -1
+        assert "formula" in _hip.last_error()
+    finally:
+        for i in ids:
+            ctx.free(i)
+    assert rel_l2(got, ref) < OP_TOL
+
+
+def test_insert_zeros_then_conv2d_is_the_reference_transpose():
+    """RMVPE's vulkan route for ConvTranspose2d (rmvpe.py:268-316): zero
+    insertion on the device, then conv2d with the flipped kernel and padding
+    1 -- the reference's formulation, zero last row and column included."""
+    from rvc_hip import _hip
+
+    ctx = _ctx()
+    L = _hip.get_lib()
+    rng = np.random.default_rng(11)
+    C_in, C_out, H, W = 24, 16, 6, 5
+    x = rng.standard_normal((1, C_in, H, W)).astype(np.float32)
+    w = (rng.standard_normal((C_in, C_out, 3, 3)) / np.sqrt(C_in * 9)).astype(np.float32)
+    wf = np.ascontiguousarray(w.transpose(1, 0, 2, 3)[:, :, ::-1, ::-1])
+    ids = [ctx.upload(x), ctx.alloc(C_in * (2 * H - 1) * (2 * W - 1)), ctx.upload(wf),
+           ctx.alloc(C_out * (2 * H - 1) * (2 * W - 1))]
+    try:
+        _hip._check(L.rvc_insert_zeros_2x(ctx.handle, ids[0], ids[1], C_in, H, W), "rvc_insert_zeros_2x")
+        xu = ctx.download(ids[1], (1, C_in, 2 * H - 1, 2 * W - 1))
+        _hip._check(L.rvc_conv2d(ctx.handle, ids[1], ids[2], 0, ids[3], 1, C_in, 2 * H - 1, 2 * W - 1, C_out, 3, 3,
+                                 1, 1, 1, 1), "rvc_conv2d")
+        y = ctx.download(ids[3], (1, C_out, 2 * H - 1, 2 * W - 1))
+    finally:
+        for i in ids:
+            ctx.free(i)
+    ref_u = np.zeros_like(xu)
+    ref_u[:, :, ::2, ::2] = x
+    np.testing.assert_array_equal(xu, ref_u)
+    ref = R.conv_transpose2d(x, w)
+    assert rel_l2(y, ref[:, :, :2 * H - 1, :2 * W - 1]) < OP_TOL
