@@ -205,16 +205,12 @@ int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, in
                      int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                      int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out);
 int32_t rvc_insert_zeros_2x(int64_t h, int64_t x, int64_t out, int64_t c, int64_t ih, int64_t iw);
-
-/* ---------------------------------------------------------------- not provided
- * Exported so the reference's loader (runtime/_vulkan.py:148-278 binds every
- * symbol) can load this library; each returns -1 with a message.  They serve
- * training and the reference's record/commit form of the RMVPE ops:
- * rvc_matmul_f16 (ffi.zig:246), rvc_batch_add_conv2d (:1196), rvc_batch_add_conv_t2d (:1246),
- * rvc_batch_add_im2col_1d (:1304), rvc_batch_add_im2col_2d (:1341),
- * rvc_batch_add_gru (:1377), rvc_batch_add_gru_sync (:1411).  RMVPE as a whole
- * runs in the rvc_rmvpe_* session below. */
-int32_t rvc_matmul_f16(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
+/* Record/commit forms (ffi.zig:1196 rvc_batch_add_conv2d, :1246
+ * rvc_batch_add_conv_t2d, :1377 rvc_batch_add_gru): the same ops appended to
+ * the pending batch and run in order by rvc_batch_commit /
+ * rvc_batch_commit_async.  rvc_batch_add_conv_t2d takes a bias b (0: none).
+ * Arguments are checked when recorded; a GRU whose step barrier gave up is
+ * reported by rvc_batch_commit / rvc_batch_wait. */
 int32_t rvc_batch_add_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
                              int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h,
                              int64_t pad_w, int64_t stride_h, int64_t stride_w);
@@ -222,12 +218,23 @@ int32_t rvc_batch_add_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t b, int64
                                int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t sh,
                                int64_t sw, int64_t ph, int64_t pw, int64_t opad_h, int64_t opad_w, int64_t h_out,
                                int64_t w_out);
+int32_t rvc_batch_add_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
+
+/* ---------------------------------------------------------------- not provided
+ * Exported so the reference's loader (runtime/_vulkan.py:148-278 binds every
+ * symbol) can load this library; each returns -1 with a message.  They serve
+ * training and the reference's record/commit form of the RMVPE ops:
+ * rvc_matmul_f16 (ffi.zig:246), rvc_batch_add_im2col_1d (:1304),
+ * rvc_batch_add_im2col_2d (:1341) and the barrier-only GRU diagnostic
+ * rvc_batch_add_gru_sync (:1411); the 2-D convs here are implicit GEMMs that
+ * need no im2col buffer.  RMVPE as a whole runs in the rvc_rmvpe_* session
+ * below. */
+int32_t rvc_matmul_f16(int64_t h, int64_t a, int64_t b, int64_t c, int64_t m, int64_t k, int64_t n);
 int32_t rvc_batch_add_im2col_1d(int64_t h, int64_t x, int64_t out, int64_t B, int64_t c, int64_t t, int64_t o_l,
                                 int64_t k_dil, int64_t stride, int64_t pad_l, int64_t dilation);
 int32_t rvc_batch_add_im2col_2d(int64_t h, int64_t x, int64_t out, int64_t B, int64_t c, int64_t ih, int64_t iw,
                                 int64_t oh, int64_t ow, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
                                 int64_t pw);
-int32_t rvc_batch_add_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim);
 int32_t rvc_batch_add_gru_sync(int64_t h, int64_t a, int64_t t, int64_t hdim);
 
 /* ---------------------------------------------------------------- synthesis session

@@ -506,6 +506,9 @@ enum SegOp : int {
   SEG_GELU = 104,
   SEG_CONV1D = 105,
   SEG_CONV_T1D = 106,
+  REC_CONV2D = 110,    // rvc_batch_add_conv2d
+  REC_CONV_T2D = 111,  // rvc_batch_add_conv_t2d
+  REC_GRU = 112,       // rvc_batch_add_gru
 };
 
 const char* kBatchCodes =
@@ -515,10 +518,179 @@ const char* kBatchCodes =
 
 bool public_code(int op) { return (op >= 1 && op <= 19); }
 
+// ---- RMVPE ops (2-D conv, transposed 2-D conv, BiGRU): checked when recorded
+// (dry), launched at commit or by the single-op exports
+
+// engine/src/engine.zig:1602-1660 (see rvc_conv2d)
+void op_conv2d(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
+               long long c_in, long long H, long long W, long long c_out, long long kh, long long kw,
+               long long pad_h, long long pad_w, long long stride_h, long long stride_w) {
+  RVC_CHECK(B >= 1 && c_in >= 1 && H >= 1 && W >= 1 && c_out >= 1 && kh >= 1 && kw >= 1 && pad_h >= 0 &&
+                pad_w >= 0 && stride_h >= 1 && stride_w >= 1,
+            "conv2d: invalid dimensions");
+  RVC_CHECK(kh <= H + 2 * pad_h && kw <= W + 2 * pad_w, "conv2d: kernel must fit the padded extent");
+  RVC_CHECK(kh <= 3 && kw <= 3 && stride_h == stride_w && stride_h <= 2,
+            "conv2d: this backend takes kernels up to 3x3 and one stride of 1 or 2 on both axes");
+  RVC_CHECK(B * c_in * H * W < (1LL << 40) && c_in <= (1 << 20) && c_out <= (1 << 20), "conv2d: too large");
+  const long long OH = (H + 2 * pad_h - kh) / stride_h + 1, OW = (W + 2 * pad_w - kw) / stride_w + 1;
+  const float* xp = e.fptr(x, B * c_in * H * W, "conv2d x");
+  const float* wp = e.fptr(w, c_out * c_in * kh * kw, "conv2d w");
+  const float* bp = b ? e.fptr(b, c_out, "conv2d b") : nullptr;
+  float* op = e.fptr(out, B * c_out * OH * OW, "conv2d out");
+  if (dry) return;
+  Conv2dLaunch a{};
+  a.n_groups = 1;
+  Conv2dGroup& g = a.g[0];
+  g.ntaps = (int)(kh * kw);
+  for (int i = 0; i < kh; ++i)
+    for (int j = 0; j < kw; ++j) {
+      g.dh[i * kw + j] = i - (int)pad_h;
+      g.dw[i * kw + j] = j - (int)pad_w;
+    }
+  g.a_lim = g.oh_n = (int)OH;
+  g.b_lim = g.ow_n = (int)OW;
+  a.x = xp; a.xb = c_in * H * W; a.xc = H * W; a.H = (int)H; a.W = (int)W;
+  a.out = op; a.ob = c_out * OH * OW; a.oc = OH * OW; a.ors = OW; a.ocs = 1;
+  a.bias = bp; a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
+  a.OH = (int)OH; a.OW = (int)OW; a.osh = a.osw = 1; a.stride = (int)stride_h;
+  const size_t wfl = (size_t)kh * kw * c_in * a.w_ld;
+  const size_t need = conv2d_split_floats(a);
+  float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (wfl + need)));
+  g.w = sc;
+  if (need > 0) {
+    a.part = sc + wfl;
+    a.part_floats = need;
+  }
+  launch_pack_conv2d_weight(wp, sc, (int)c_out, (int)c_in, (int)kh, (int)kw, e.stream);
+  launch_conv2d(a, e.stream);
+}
+
+// engine/src/engine.zig:1511-1560 (see rvc_conv_t2d); b == 0: no bias
+void op_conv_t2d(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
+                 long long c_in, long long ih, long long iw, long long c_out, long long kh, long long kw, long long sh,
+                 long long sw, long long ph, long long pw, long long opad_h, long long opad_w, long long h_out,
+                 long long w_out) {
+  RVC_CHECK(B >= 1 && c_in >= 1 && ih >= 1 && iw >= 1 && c_out >= 1 && kh >= 1 && kw >= 1 && sh >= 1 && sw >= 1 &&
+                ph >= 0 && pw >= 0 && opad_h >= 0 && opad_w >= 0,
+            "conv_t2d: invalid dimensions");
+  RVC_CHECK(opad_h < sh && opad_w < sw, "conv_t2d: output padding must be smaller than the stride");
+  const long long hext = (ih - 1) * sh + (kh - 1), wext = (iw - 1) * sw + (kw - 1);
+  RVC_CHECK(2 * ph <= hext && 2 * pw <= wext, "conv_t2d: padding must fit the upsampled extent");
+  RVC_CHECK(h_out == hext + opad_h + 1 - 2 * ph && w_out == wext + opad_w + 1 - 2 * pw,
+            "conv_t2d: h_out / w_out do not match the transposed-conv formula");
+  RVC_CHECK(kh <= 3 && kw <= 3 && sh <= 2 && sw <= 2, "conv_t2d: this backend takes kernels up to 3x3 and strides up to 2");
+  RVC_CHECK(B * c_in * ih * iw < (1LL << 40) && c_in <= (1 << 20) && c_out <= (1 << 20) && h_out * w_out < (1LL << 31),
+            "conv_t2d: too large");
+  const float* xp = e.fptr(x, B * c_in * ih * iw, "conv_t2d x");
+  const float* wp = e.fptr(w, c_in * c_out * kh * kw, "conv_t2d w");
+  const float* bp = b ? e.fptr(b, c_out, "conv_t2d b") : nullptr;
+  float* op = e.fptr(out, B * c_out * h_out * w_out, "conv_t2d out");
+  if (dry) return;
+  Conv2dLaunch a{};
+  ConvT2dTaps taps[kConv2dGroupsMax];
+  int maxh = 0, maxw = 0;
+  for (int c = 0; c < sh; ++c)
+    for (int d = 0; d < sw; ++d) {
+      const int oh_n = c < h_out ? (int)((h_out - c + sh - 1) / sh) : 0;
+      const int ow_n = d < w_out ? (int)((w_out - d + sw - 1) / sw) : 0;
+      if (oh_n == 0 || ow_n == 0) continue;
+      Conv2dGroup& g = a.g[a.n_groups];
+      ConvT2dTaps& t = taps[a.n_groups];
+      t.n = 0;
+      for (int i = 0; i < kh; ++i) {
+        if ((c + ph - i) % sh != 0) continue;
+        for (int j = 0; j < kw; ++j) {
+          if ((d + pw - j) % sw != 0) continue;
+          t.kh[t.n] = i;
+          t.kw[t.n] = j;
+          g.dh[t.n] = (int)((c + ph - i) / sh);
+          g.dw[t.n] = (int)((d + pw - j) / sw);
+          ++t.n;
+        }
+      }
+      if (t.n == 0) {  // no tap reaches this phase: bias only
+        t.n = 1;
+        t.kh[0] = t.kw[0] = -1;
+        g.dh[0] = g.dw[0] = 0;
+      }
+      g.ntaps = t.n;
+      g.oh0 = c;
+      g.ow0 = d;
+      g.a_lim = g.oh_n = oh_n;
+      g.b_lim = g.ow_n = ow_n;
+      maxh = std::max(maxh, oh_n);
+      maxw = std::max(maxw, ow_n);
+      ++a.n_groups;
+    }
+  a.x = xp; a.xb = c_in * ih * iw; a.xc = ih * iw; a.H = (int)ih; a.W = (int)iw;
+  a.out = op; a.ob = c_out * h_out * w_out; a.oc = h_out * w_out; a.ors = w_out; a.ocs = 1;
+  a.bias = bp; a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
+  a.OH = maxh; a.OW = maxw; a.osh = (int)sh; a.osw = (int)sw; a.stride = 1;
+  size_t wfl = 0;
+  for (int gi = 0; gi < a.n_groups; ++gi) wfl += (size_t)taps[gi].n * c_in * a.w_ld;
+  const size_t need = conv2d_split_floats(a);
+  float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (wfl + need)));
+  size_t off = 0;
+  for (int gi = 0; gi < a.n_groups; ++gi) {
+    a.g[gi].w = sc + off;
+    launch_pack_convt2d_phase(wp, sc + off, (int)c_in, (int)c_out, (int)kh, (int)kw, taps[gi], e.stream);
+    off += (size_t)taps[gi].n * c_in * a.w_ld;
+  }
+  if (need > 0) {
+    a.part = sc + wfl;
+    a.part_floats = need;
+  }
+  launch_conv2d(a, e.stream);
+}
+
+// engine/src/engine.zig:3097-3112 (see rvc_gru); the error flag is checked
+// after the next synchronisation (check_gru)
+void op_gru(Engine& e, bool dry, long long a_, long long b_, long long c_, long long out, long long t,
+            long long hdim) {
+  RVC_CHECK(t >= 1 && hdim >= 1 && hdim <= 256 && t < (1LL << 30), "gru: need T >= 1 and 1 <= H <= 256");
+  const long long k = 3 * hdim;
+  GruArgs g{};
+  g.gx = e.fptr(a_, 2 * t * k, "gru gx");
+  g.whh = e.fptr(b_, 2 * k * hdim, "gru w_hh");
+  g.bhh = e.fptr(c_, 2 * k, "gru b_hh");
+  g.out = e.fptr(out, t * 2 * hdim, "gru out");
+  if (dry) return;
+  g.g_d = t * k; g.g_t = k; g.g_r = 1;
+  g.o_d = hdim; g.o_t = 2 * hdim; g.o_j = 1;
+  g.T = (int)t; g.H = (int)hdim; g.spin_limit = 1LL << 22;
+  if (!e.gru_state) {
+    void* p = nullptr;
+    RVC_HIP(hipMalloc(&p, sizeof(unsigned long long) * (2 * 2 * 256 + 2)));
+    e.gru_state = static_cast<unsigned long long*>(p);
+  }
+  g.state = e.gru_state;
+  g.sync = reinterpret_cast<unsigned*>(e.gru_state + 2 * 2 * 256);
+  launch_bigru(g, e.stream);  // its init kernel clears the flag first
+  e.gru_pending = true;
+}
+
+// After a synchronisation: report a GRU launch whose step barrier gave up.
+void check_gru(Engine& e) {
+  if (!e.gru_pending) return;
+  e.gru_pending = false;
+  unsigned flag = 0;
+  RVC_HIP(hipMemcpy(&flag, reinterpret_cast<unsigned*>(e.gru_state + 2 * 2 * 256) + 2, sizeof(unsigned),
+                    hipMemcpyDeviceToHost));
+  RVC_CHECK(flag == 0, "gru: step barrier timed out (workgroups not co-resident)");
+}
+
 void run_batch_op(Engine& e, const BatchOp& o, bool dry) {
   const long long* p = o.p;
   switch (o.op) {
     case 1: op_matmul(e, dry, o.a, o.b, o.c, p[0], p[1], p[2]); break;
+    case REC_CONV2D:
+      op_conv2d(e, dry, o.a, o.b, o.c, p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10], p[11]);
+      break;
+    case REC_CONV_T2D:
+      op_conv_t2d(e, dry, o.a, o.b, o.c, p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], p[9], p[10], p[11],
+                  p[12], p[13], p[14], p[15]);
+      break;
+    case REC_GRU: op_gru(e, dry, o.a, o.b, o.c, p[0], p[1], p[2]); break;
     case 2: op_conv1d(e, dry, o.a, o.b, o.c, p[9], p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8]); break;
     case 3:
     case 4: {
@@ -956,6 +1128,7 @@ int32_t rvc_batch_commit(int64_t h) {
     commit_batch(e);
     e.sync();
     e.in_flight = false;
+    check_gru(e);
   });
 }
 
@@ -970,6 +1143,7 @@ int32_t rvc_batch_wait(int64_t h) {
   return guarded(h, [&](Engine& e) {
     e.sync();
     e.in_flight = false;
+    check_gru(e);
   });
 }
 
@@ -1110,47 +1284,8 @@ int32_t rvc_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
                    int64_t W, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h, int64_t pad_w, int64_t stride_h,
                    int64_t stride_w) {
   return guarded(h, [&](Engine& e) {
-    RVC_CHECK(B >= 1 && c_in >= 1 && H >= 1 && W >= 1 && c_out >= 1 && kh >= 1 && kw >= 1 && pad_h >= 0 &&
-                  pad_w >= 0 && stride_h >= 1 && stride_w >= 1,
-              "conv2d: invalid dimensions");
-    RVC_CHECK(kh <= H + 2 * pad_h && kw <= W + 2 * pad_w, "conv2d: kernel must fit the padded extent");
-    RVC_CHECK(kh <= 3 && kw <= 3 && stride_h == stride_w && stride_h <= 2,
-              "conv2d: this backend takes kernels up to 3x3 and one stride of 1 or 2 on both axes");
-    RVC_CHECK(B * c_in * H * W < (1LL << 40) && c_in <= (1 << 20) && c_out <= (1 << 20), "conv2d: too large");
-    const long long OH = (H + 2 * pad_h - kh) / stride_h + 1, OW = (W + 2 * pad_w - kw) / stride_w + 1;
-    const float* xp = e.fptr(x, B * c_in * H * W, "conv2d x");
-    const float* wp = e.fptr(w, c_out * c_in * kh * kw, "conv2d w");
-    const float* bp = b ? e.fptr(b, c_out, "conv2d b") : nullptr;
-    float* op = e.fptr(out, B * c_out * OH * OW, "conv2d out");
-    Conv2dLaunch a{};
-    a.n_groups = 1;
-    Conv2dGroup& g = a.g[0];
-    g.ntaps = (int)(kh * kw);
-    for (int i = 0; i < kh; ++i)
-      for (int j = 0; j < kw; ++j) {
-        g.dh[i * kw + j] = i - (int)pad_h;
-        g.dw[i * kw + j] = j - (int)pad_w;
-      }
-    g.a_lim = (int)OH;
-    g.b_lim = (int)OW;
-    g.oh_n = (int)OH;
-    g.ow_n = (int)OW;
-    a.x = xp; a.xb = c_in * H * W; a.xc = H * W; a.H = (int)H; a.W = (int)W;
-    a.out = op; a.ob = c_out * OH * OW; a.oc = OH * OW; a.ors = OW; a.ocs = 1;
-    a.bias = bp; a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
-    a.OH = (int)OH; a.OW = (int)OW; a.osh = a.osw = 1; a.stride = (int)stride_h;
-    const size_t wfl = (size_t)kh * kw * c_in * a.w_ld;
-    const size_t need = conv2d_split_floats(a);
-    float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (wfl + need)));
-    g.w = sc;
-    if (need > 0) {
-      a.part = sc + wfl;
-      a.part_floats = need;
-    }
-    submit(e, [&] {
-      launch_pack_conv2d_weight(wp, sc, (int)c_out, (int)c_in, (int)kh, (int)kw, e.stream);
-      launch_conv2d(a, e.stream);
-    });
+    op_conv2d(e, true, x, w, b, out, B, c_in, H, W, c_out, kh, kw, pad_h, pad_w, stride_h, stride_w);
+    submit(e, [&] { op_conv2d(e, false, x, w, b, out, B, c_in, H, W, c_out, kh, kw, pad_h, pad_w, stride_h, stride_w); });
   });
 }
 // engine/src/ffi.zig:428-479 + engine.zig:1511-1560: out[B][C_out][h_out][w_out]
@@ -1164,78 +1299,10 @@ int32_t rvc_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t out, int64_t B, in
                      int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                      int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out) {
   return guarded(h, [&](Engine& e) {
-    RVC_CHECK(B >= 1 && c_in >= 1 && ih >= 1 && iw >= 1 && c_out >= 1 && kh >= 1 && kw >= 1 && sh >= 1 && sw >= 1 &&
-                  ph >= 0 && pw >= 0 && opad_h >= 0 && opad_w >= 0,
-              "conv_t2d: invalid dimensions");
-    RVC_CHECK(opad_h < sh && opad_w < sw, "conv_t2d: output padding must be smaller than the stride");
-    const long long hext = (ih - 1) * sh + (kh - 1), wext = (iw - 1) * sw + (kw - 1);
-    RVC_CHECK(2 * ph <= hext && 2 * pw <= wext, "conv_t2d: padding must fit the upsampled extent");
-    RVC_CHECK(h_out == hext + opad_h + 1 - 2 * ph && w_out == wext + opad_w + 1 - 2 * pw,
-              "conv_t2d: h_out / w_out do not match the transposed-conv formula");
-    RVC_CHECK(kh <= 3 && kw <= 3 && sh <= 2 && sw <= 2, "conv_t2d: this backend takes kernels up to 3x3 and strides up to 2");
-    RVC_CHECK(B * c_in * ih * iw < (1LL << 40) && c_in <= (1 << 20) && c_out <= (1 << 20) && h_out * w_out < (1LL << 31),
-              "conv_t2d: too large");
-    const float* xp = e.fptr(x, B * c_in * ih * iw, "conv_t2d x");
-    const float* wp = e.fptr(w, c_in * c_out * kh * kw, "conv_t2d w");
-    float* op = e.fptr(out, B * c_out * h_out * w_out, "conv_t2d out");
-    Conv2dLaunch a{};
-    ConvT2dTaps taps[kConv2dGroupsMax];
-    int maxh = 0, maxw = 0;
-    for (int c = 0; c < sh; ++c)
-      for (int d = 0; d < sw; ++d) {
-        const int oh_n = c < h_out ? (int)((h_out - c + sh - 1) / sh) : 0;
-        const int ow_n = d < w_out ? (int)((w_out - d + sw - 1) / sw) : 0;
-        if (oh_n == 0 || ow_n == 0) continue;
-        Conv2dGroup& g = a.g[a.n_groups];
-        ConvT2dTaps& t = taps[a.n_groups];
-        t.n = 0;
-        for (int i = 0; i < kh; ++i) {
-          if ((c + ph - i) % sh != 0) continue;
-          for (int j = 0; j < kw; ++j) {
-            if ((d + pw - j) % sw != 0) continue;
-            t.kh[t.n] = i;
-            t.kw[t.n] = j;
-            g.dh[t.n] = (int)((c + ph - i) / sh);
-            g.dw[t.n] = (int)((d + pw - j) / sw);
-            ++t.n;
-          }
-        }
-        if (t.n == 0) {  // no tap reaches this phase: zeros
-          t.n = 1;
-          t.kh[0] = t.kw[0] = -1;
-          g.dh[0] = g.dw[0] = 0;
-        }
-        g.ntaps = t.n;
-        g.oh0 = c;
-        g.ow0 = d;
-        g.a_lim = g.oh_n = oh_n;
-        g.b_lim = g.ow_n = ow_n;
-        maxh = std::max(maxh, oh_n);
-        maxw = std::max(maxw, ow_n);
-        ++a.n_groups;
-      }
-    a.x = xp; a.xb = c_in * ih * iw; a.xc = ih * iw; a.H = (int)ih; a.W = (int)iw;
-    a.out = op; a.ob = c_out * h_out * w_out; a.oc = h_out * w_out; a.ors = w_out; a.ocs = 1;
-    a.C_in = (int)c_in; a.C_out = (int)c_out; a.w_ld = packed_ld((int)c_out); a.B = (int)B;
-    a.OH = maxh; a.OW = maxw; a.osh = (int)sh; a.osw = (int)sw; a.stride = 1;
-    size_t wfl = 0;
-    for (int gi = 0; gi < a.n_groups; ++gi) wfl += (size_t)taps[gi].n * c_in * a.w_ld;
-    const size_t need = conv2d_split_floats(a);
-    float* sc = static_cast<float*>(e.scratch_for(sizeof(float) * (wfl + need)));
-    size_t off = 0;
-    for (int gi = 0; gi < a.n_groups; ++gi) {
-      a.g[gi].w = sc + off;
-      off += (size_t)taps[gi].n * c_in * a.w_ld;
-    }
-    if (need > 0) {
-      a.part = sc + wfl;
-      a.part_floats = need;
-    }
+    op_conv_t2d(e, true, x, w, 0, out, B, c_in, ih, iw, c_out, kh, kw, sh, sw, ph, pw, opad_h, opad_w, h_out, w_out);
     submit(e, [&] {
-      for (int gi = 0; gi < a.n_groups; ++gi)
-        launch_pack_convt2d_phase(wp, const_cast<float*>(a.g[gi].w), (int)c_in, (int)c_out, (int)kh, (int)kw, taps[gi],
-                                  e.stream);
-      launch_conv2d(a, e.stream);
+      op_conv_t2d(e, false, x, w, 0, out, B, c_in, ih, iw, c_out, kh, kw, sh, sw, ph, pw, opad_h, opad_w, h_out,
+                  w_out);
     });
   });
 }
@@ -1251,14 +1318,19 @@ int32_t rvc_insert_zeros_2x(int64_t h, int64_t x, int64_t out, int64_t c, int64_
     submit(e, [&] { launch_insert_zeros_2x(xp, op, c, (int)h_, (int)w, e.stream); });
   });
 }
-int32_t rvc_batch_add_conv2d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                             int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
-  return not_provided("rvc_batch_add_conv2d");
+// engine/src/ffi.zig:1196-1244: rvc_conv2d recorded into the pending batch
+int32_t rvc_batch_add_conv2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                             int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t pad_h,
+                             int64_t pad_w, int64_t stride_h, int64_t stride_w) {
+  return record(h, BatchOp{REC_CONV2D, x, w, b, {out, B, c_in, ih, iw, c_out, kh, kw, pad_h, pad_w, stride_h, stride_w}});
 }
-int32_t rvc_batch_add_conv_t2d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                               int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                               int64_t, int64_t) {
-  return not_provided("rvc_batch_add_conv_t2d");
+// engine/src/ffi.zig:1246-1302: rvc_conv_t2d with a bias (b == 0: none),
+// recorded into the pending batch
+int32_t rvc_batch_add_conv_t2d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                               int64_t ih, int64_t iw, int64_t c_out, int64_t kh, int64_t kw, int64_t sh, int64_t sw,
+                               int64_t ph, int64_t pw, int64_t opad_h, int64_t opad_w, int64_t h_out, int64_t w_out) {
+  return record(h, BatchOp{REC_CONV_T2D, x, w, b,
+                           {out, B, c_in, ih, iw, c_out, kh, kw, sh, sw, ph, pw, opad_h, opad_w, h_out, w_out}});
 }
 int32_t rvc_batch_add_im2col_1d(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                                 int64_t, int64_t) {
@@ -1268,8 +1340,10 @@ int32_t rvc_batch_add_im2col_2d(int64_t, int64_t, int64_t, int64_t, int64_t, int
                                 int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
   return not_provided("rvc_batch_add_im2col_2d");
 }
-int32_t rvc_batch_add_gru(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t) {
-  return not_provided("rvc_batch_add_gru");
+// engine/src/ffi.zig:1377-1392: rvc_gru recorded into the pending batch (its
+// barrier flag is checked by rvc_batch_commit / rvc_batch_wait)
+int32_t rvc_batch_add_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim) {
+  return record(h, BatchOp{REC_GRU, a, b, c, {out, t, hdim}});
 }
 // engine/src/ffi.zig:1394-1409 + engine.zig:3097-3112: bidirectional GRU
 // recurrence over precomputed gate inputs a [2T][3H] (rows 0..T-1 forward,
@@ -1277,24 +1351,10 @@ int32_t rvc_batch_add_gru(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, 
 // [2][3H]; out [T][2H] (forward units first).  H <= 256 as in the reference.
 int32_t rvc_gru(int64_t h, int64_t a, int64_t b, int64_t c, int64_t out, int64_t t, int64_t hdim) {
   return guarded(h, [&](Engine& e) {
-    RVC_CHECK(t >= 1 && hdim >= 1 && hdim <= 256 && t < (1LL << 30), "gru: need T >= 1 and 1 <= H <= 256");
-    const long long k = 3 * hdim;
-    GruArgs g{};
-    g.gx = e.fptr(a, 2 * t * k, "gru gx");
-    g.whh = e.fptr(b, 2 * k * hdim, "gru w_hh");
-    g.bhh = e.fptr(c, 2 * k, "gru b_hh");
-    g.out = e.fptr(out, t * 2 * hdim, "gru out");
-    g.g_d = t * k; g.g_t = k; g.g_r = 1;
-    g.o_d = hdim; g.o_t = 2 * hdim; g.o_j = 1;
-    g.T = (int)t; g.H = (int)hdim; g.spin_limit = 1LL << 22;
-    auto* sc = static_cast<unsigned long long*>(e.scratch_for(sizeof(unsigned long long) * (2 * 2 * 256 + 2)));
-    g.state = sc;
-    g.sync = reinterpret_cast<unsigned*>(sc + 2 * 2 * 256);
-    submit(e, [&] { launch_bigru(g, e.stream); });
-    unsigned flag = 0;
-    RVC_HIP(hipMemcpyAsync(&flag, g.sync + 2, sizeof(unsigned), hipMemcpyDeviceToHost, e.stream));
+    op_gru(e, true, a, b, c, out, t, hdim);
+    submit(e, [&] { op_gru(e, false, a, b, c, out, t, hdim); });
     e.sync();
-    RVC_CHECK(flag == 0, "gru: step barrier timed out (workgroups not co-resident)");
+    check_gru(e);
   });
 }
 int32_t rvc_batch_add_gru_sync(int64_t, int64_t, int64_t, int64_t) { return not_provided("rvc_batch_add_gru_sync"); }

@@ -31,6 +31,11 @@ struct Engine {
   // scratch for packed weights of op-level calls
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // BiGRU exchange words + error flag of rvc_gru / rvc_batch_add_gru (kept
+  // apart from the scratch, which later ops of a batch reuse), and whether a
+  // launched GRU's flag still awaits its check after the next sync
+  unsigned long long* gru_state = nullptr;
+  bool gru_pending = false;
   // record/commit batch
   std::vector<BatchOp> batch;
   bool in_flight = false;

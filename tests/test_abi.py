@@ -118,8 +118,8 @@ def test_reference_loader_symbols_bind(hip):
 
 def test_not_provided_exports_fail_with_message(hip):
     L = hip.get_lib()
-    assert L.rvc_batch_add_conv_t2d(1, *([1] * 19)) == -1
-    assert "rvc_batch_add_conv_t2d: not provided" in hip.last_error()
+    assert L.rvc_batch_add_gru_sync(1, 1, 1, 1) == -1
+    assert "rvc_batch_add_gru_sync: not provided" in hip.last_error()
     assert L.rvc_matmul_f16(1, 1, 1, 1, 1, 1, 1) == -1
     assert "rvc_matmul_f16: not provided" in hip.last_error()
     assert L.rvc_batch_add_im2col_2d(1, *([1] * 14)) == -1
@@ -149,6 +149,12 @@ def test_new_exports_reject_bad_handles(hip):
     assert L.rvc_conv_t2d(424242, *([1] * 18)) == -1
     assert hip.last_error() == "invalid engine handle"
     assert L.rvc_insert_zeros_2x(424242, 1, 2, 1, 1, 1) == -1
+    assert hip.last_error() == "invalid engine handle"
+    assert L.rvc_batch_add_conv2d(424242, *([1] * 15)) == -1
+    assert hip.last_error() == "invalid engine handle"
+    assert L.rvc_batch_add_conv_t2d(424242, *([1] * 19)) == -1
+    assert hip.last_error() == "invalid engine handle"
+    assert L.rvc_batch_add_gru(424242, 1, 1, 1, 1, 1, 1) == -1
     assert hip.last_error() == "invalid engine handle"
     assert L.rvc_rmvpe_create(424242) == -1
     assert L.rvc_rmvpe_finalize(424242) == -1

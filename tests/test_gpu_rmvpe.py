@@ -287,3 +287,72 @@ def test_insert_zeros_then_conv2d_is_the_reference_transpose():
     np.testing.assert_array_equal(xu, ref_u)
     ref = R.conv_transpose2d(x, w)
     assert rel_l2(y, ref[:, :, :2 * H - 1, :2 * W - 1]) < OP_TOL
+
+
+def test_batched_2d_ops_match_single_ops():
+    """rvc_batch_add_{conv2d,conv_t2d,gru} (ffi.zig:1196, :1246, :1377): one
+    batch that chains conv2d -> conv_t2d (with a bias) and runs a BiGRU gives
+    the single-op results, checked against torch and the oracle; a record the
+    backend cannot run is refused when it is added, not at commit."""
+    import torch
+
+    from rvc_hip import _hip
+
+    ctx = _ctx()
+    L = _hip.get_lib()
+    rng = np.random.default_rng(5)
+    C0, C1, C2, H, W = 16, 24, 8, 7, 10
+    x = rng.standard_normal((1, C0, H, W)).astype(np.float32)
+    w1 = (rng.standard_normal((C1, C0, 3, 3)) / np.sqrt(C0 * 9)).astype(np.float32)
+    b1 = rng.standard_normal(C1).astype(np.float32)
+    w2 = (rng.standard_normal((C1, C2, 3, 3)) / np.sqrt(C1 * 9)).astype(np.float32)
+    b2 = rng.standard_normal(C2).astype(np.float32)
+    T, Hd = 23, 32
+    bound = 1.0 / np.sqrt(Hd)
+    gx = rng.uniform(-1, 1, (2 * T, 3 * Hd)).astype(np.float32)
+    whh = rng.uniform(-bound, bound, (2, 3 * Hd, Hd)).astype(np.float32)
+    bhh = rng.uniform(-bound, bound, (2, 3 * Hd)).astype(np.float32)
+    y1_ref = R.conv2d(x, w1, b1, 1)
+    y2_ref = torch.nn.functional.conv_transpose2d(torch.from_numpy(y1_ref), torch.from_numpy(w2),
+                                                  torch.from_numpy(b2), stride=2, padding=1,
+                                                  output_padding=1).numpy()
+    OH, OW = 2 * H, 2 * W
+    # gate inputs handed over directly: the oracle's W_ih selects each direction's half of [T][6H]
+    sel = np.eye(6 * Hd, dtype=np.float32)
+    zb = np.zeros(3 * Hd, np.float32)
+    g_ref = R.bigru(np.concatenate([gx[:T], gx[T:]], axis=1), sel[:3 * Hd], whh[0], zb, bhh[0], sel[3 * Hd:],
+                    whh[1], zb, bhh[1])
+    ids = {k: ctx.upload(v) for k, v in (("x", x), ("w1", w1), ("b1", b1), ("w2", w2), ("b2", b2), ("gx", gx),
+                                         ("whh", whh), ("bhh", bhh))}
+    ids["y1"] = ctx.alloc(C1 * H * W)
+    ids["y2"] = ctx.alloc(C2 * OH * OW)
+    ids["g"] = ctx.alloc(T * 2 * Hd)
+    try:
+        print("batched conv2d -> conv_t2d + gru", flush=True)
+        _hip._check(L.rvc_batch_begin(ctx.handle), "rvc_batch_begin")
+        _hip._check(L.rvc_batch_add_conv2d(ctx.handle, ids["x"], ids["w1"], ids["b1"], ids["y1"], 1, C0, H, W, C1,
+                                           3, 3, 1, 1, 1, 1), "rvc_batch_add_conv2d")
+        assert L.rvc_batch_add_conv2d(ctx.handle, ids["x"], ids["w1"], 0, ids["y1"], 1, C0, H, W, C1, 5, 5, 2, 2,
+                                      1, 1) == -1
+        assert "3x3" in _hip.last_error()
+        _hip._check(L.rvc_batch_add_conv_t2d(ctx.handle, ids["y1"], ids["w2"], ids["b2"], ids["y2"], 1, C1, H, W,
+                                             C2, 3, 3, 2, 2, 1, 1, 1, 1, OH, OW), "rvc_batch_add_conv_t2d")
+        _hip._check(L.rvc_batch_add_gru(ctx.handle, ids["gx"], ids["whh"], ids["bhh"], ids["g"], T, Hd),
+                    "rvc_batch_add_gru")
+        _hip._check(L.rvc_batch_commit(ctx.handle), "rvc_batch_commit")
+        y1 = ctx.download(ids["y1"], y1_ref.shape)
+        y2 = ctx.download(ids["y2"], y2_ref.shape)
+        g = ctx.download(ids["g"], (T, 2 * Hd))
+        _hip._check(L.rvc_conv2d(ctx.handle, ids["x"], ids["w1"], ids["b1"], ids["y1"], 1, C0, H, W, C1, 3, 3, 1, 1,
+                                 1, 1), "rvc_conv2d")
+        _hip._check(L.rvc_gru(ctx.handle, ids["gx"], ids["whh"], ids["bhh"], ids["g"], T, Hd), "rvc_gru")
+        y1s = ctx.download(ids["y1"], y1_ref.shape)
+        gs = ctx.download(ids["g"], (T, 2 * Hd))
+    finally:
+        for i in ids.values():
+            ctx.free(i)
+    np.testing.assert_array_equal(y1, y1s)
+    np.testing.assert_array_equal(g, gs)
+    assert rel_l2(y1, y1_ref) < OP_TOL
+    assert rel_l2(y2, y2_ref) < OP_TOL
+    np.testing.assert_allclose(g, g_ref, rtol=0, atol=1e-5)
