@@ -417,7 +417,7 @@ __device__ __forceinline__ void persist_tile(int lin, int n_tx, int n_ty, int& t
 template <int BM, int BN, int WM, int WN, int BK, int FAM>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(4)))
-void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floats) {
+void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floats, int cpx) {
   using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = BK;
   constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
@@ -427,7 +427,6 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   const int per_group = a.B * per_b;
   const int n_items = per_group * a.n_groups;
   int item = blockIdx.x;
-  if (item >= n_items) return;  // uniform for the whole workgroup, before any barrier
   const int nchunk = a.C_in / BKT;  // the launcher requires C_in % BK == 0
   // Item scheduling.  Static: slot s runs items s, s + grid, ...  Dynamic
   // (a.queue): every workgroup starts on item blockIdx.x, then takes tickets
@@ -439,6 +438,21 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   const int nq = gridDim.x % 8 == 0 ? 8 : 1;
   const int qx = blockIdx.x % nq;
   const int per_q = gridDim.x / nq;
+  // First items in snake order: workgroup q of an XCD class (q = blockIdx / 8)
+  // is dispatched to about CU q % cpx of that XCD, in round s = q / cpx; odd
+  // rounds take their run of the heaviest-first item list in reverse, so a
+  // CU that drew a heavy item in one round draws a light one in the next.
+  // A permutation of [0, gridDim) that keeps blockIdx % 8, so the static
+  // stride and the ticket queues still cover every item once.
+  if (cpx > 0 && nq == 8) {
+    const int q = (int)blockIdx.x / 8;
+    const int r = q / cpx;
+    if (r & 1) {
+      const int n_r = min(cpx, per_q - r * cpx);
+      item = (r * cpx + (n_r - 1 - (q - r * cpx))) * 8 + qx;
+    }
+  }
+  if (item >= n_items) return;  // uniform for the whole workgroup, before any barrier
 
   extern __shared__ float smem[];
   const int tid = threadIdx.x;
@@ -856,12 +870,13 @@ bool launch_persist(const ConvLaunch& a, hipStream_t s) {
   long long grid = (long long)per_cu * device_cus();
   if (grid >= 8) grid -= grid % 8;  // item j then runs on XCD j % 8
   grid = std::min(grid, items);
+  const int cpx = device_cus() % 8 == 0 ? device_cus() / 8 : 0;  // CUs per XCD
   if (fam)
     hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1>), dim3((unsigned)grid), dim3(C::NT), lds,
-                       s, a, n_tx, n_ty, stage);
+                       s, a, n_tx, n_ty, stage, cpx);
   else
     hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0>), dim3((unsigned)grid), dim3(C::NT), lds,
-                       s, a, n_tx, n_ty, stage);
+                       s, a, n_tx, n_ty, stage, cpx);
   check_launch("conv1d_mfma_persist");
   return true;
 }
