@@ -2,7 +2,8 @@
 //   * strided conv1d with few input channels (the NSF noise convs,
 //     1 -> C with k = 2*stride; runtime/models/vits.py:1628-1635),
 //   * conv_post (32 -> 1, k7, leaky 0.01 prologue, tanh epilogue;
-//     runtime/models/vits.py:2228-2231),
+//     runtime/models/vits.py:2228-2231) and other stride-1 launches with
+//     fewer than 8 output channels, staged through LDS rows,
 //   * the general op-level conv1d (stride > 1) and ConvTranspose1d with
 //     dilation / output_padding (runtime/nn.py:89-135, 293-346).
 // Plus the device-side weight packers for the MFMA kernel.
@@ -63,6 +64,56 @@ __global__ __launch_bounds__(256) void conv1d_direct_kernel(DirectConvArgs a) {
     else if (a.combine == COMB_ADD_DIV) v = (*o + v) / a.div;
     *o = v;
   }
+}
+
+// Stride-1 convolution with few output channels (conv_post: 32 -> 1, k7):
+// a workgroup owns 256 consecutive outputs of one output channel and walks
+// the input channels kRowCh at a time, staging each channel's 256 + halo
+// samples in LDS once (coalesced, input activation applied on the way in).
+// Thread t computes output t, so a wave reads 64 neighbouring LDS words per
+// tap; the small tile keeps several workgroups per CU in flight to hide the
+// load latency of each chunk.  Per output the sum runs channel-major, taps
+// inner, as in conv1d_direct_kernel.
+constexpr int kRowOut = 256, kRowCh = 8, kRowHaloMax = 128;
+__global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
+  __shared__ float rows[kRowCh][kRowOut + kRowHaloMax];
+  const int i0 = blockIdx.x * kRowOut;
+  const int co = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int W = kRowOut + (a.K - 1) * a.dil;  // launcher: (K - 1) * dil <= kRowHaloMax
+  const float* xb = a.x + (long long)b * a.xb;
+  const long long tb = (long long)i0 + a.in_off;
+  float acc = 0.f;
+  for (int ci0 = 0; ci0 < a.C_in; ci0 += kRowCh) {
+    const int nch = min(kRowCh, a.C_in - ci0);
+    for (int r = 0; r < nch; ++r) {
+      const float* xr = xb + (long long)(ci0 + r) * a.xc;
+      for (int c = tid; c < W; c += 256) {
+        const long long t = tb + c;
+        rows[r][c] = (t >= 0 && t < a.L_in) ? act_in(xr[t], a.in_act, a.in_slope) : 0.f;
+      }
+    }
+    __syncthreads();
+    for (int r = 0; r < nch; ++r) {
+      const float* wr = a.w + ((long long)co * a.C_in + ci0 + r) * a.K;
+      for (int k = 0; k < a.K; ++k) {
+        const float wv = wr[k];
+        acc += wv * rows[r][tid + k * a.dil];
+      }
+    }
+    __syncthreads();
+  }
+  float* ob = a.out + (long long)b * a.ob + (long long)co * a.oc;
+  const int i = i0 + tid;
+  if (i >= a.n_out) return;
+  float v = acc;
+  if (a.bias) v = v + a.bias[co];
+  v = act_out(v, a.out_act, a.out_slope);
+  float* o = ob + i;
+  if (a.combine == COMB_ADD) v = *o + v;
+  else if (a.combine == COMB_ADD_DIV) v = (*o + v) / a.div;
+  *o = v;
 }
 
 // Gather-form ConvTranspose1d: one thread per output element.
@@ -157,6 +208,9 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
   if (a.C_out >= 8) {
     dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);
     hipLaunchKernelGGL(conv1d_direct_kernel<8>, grid, dim3(256), 0, s, a);
+  } else if (a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax) {
+    dim3 grid((a.n_out + kRowOut - 1) / kRowOut, a.C_out, a.B);
+    hipLaunchKernelGGL(conv1d_rows_kernel, grid, dim3(256), 0, s, a);
   } else {
     dim3 grid((a.n_out + 255) / 256, a.C_out, a.B);
     hipLaunchKernelGGL(conv1d_direct_kernel<1>, grid, dim3(256), 0, s, a);
