@@ -388,6 +388,7 @@ int32_t rvc_hubert_encode(int64_t hh, const float* x, int64_t B, int64_t T, int3
     float* dout = s.buf("out", (size_t)n_out);
     RVC_HIP(hipMemcpyAsync(dx, x, sizeof(float) * B * T, hipMemcpyHostToDevice, st));
     s.encode(dx, (int)B, T, version, dout);
+    s.close_span();
     RVC_HIP(hipMemcpyAsync(out, dout, sizeof(float) * n_out, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
     s.collect_timing();
@@ -402,6 +403,7 @@ int32_t rvc_hubert_encode_dev(int64_t hh, int64_t x, int64_t B, int64_t T, int32
     const float* xp = e.fptr(x, B * T, "hubert x");
     float* op = e.fptr(out, B * L * s.out_dim(version), "hubert out");
     s.encode(xp, (int)B, T, version, op);
+    s.close_span();
     e.sync();
     s.collect_timing();
   });

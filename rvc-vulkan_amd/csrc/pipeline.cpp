@@ -253,6 +253,7 @@ int32_t rvc_vc_search(int64_t vh, const float* query, int64_t F, int64_t k, floa
     long long* ix = reinterpret_cast<long long*>(v.buf("out_ix", (size_t)F * k * 2));
     h2d(q, query, sizeof(float) * (size_t)F * v.D, s);
     v.search(q, (int)F, (int)k, sc, ix);
+    v.close_span();
     d2h(scores, sc, sizeof(float) * (size_t)F * k, s);
     d2h(inds, ix, sizeof(long long) * (size_t)F * k, s);
     v.eng->sync();
@@ -269,6 +270,7 @@ int32_t rvc_vc_search_dev(int64_t vh, int64_t query, int64_t F, int64_t k, int64
     float* sc = e.fptr(scores, F * k, "search scores");
     long long* ix = reinterpret_cast<long long*>(e.fptr(inds, F * k * 2, "search indices (int64)"));
     v.search(q, (int)F, (int)k, sc, ix);
+    v.close_span();
     e.sync();
     v.collect_timing();
   });
@@ -287,6 +289,7 @@ int32_t rvc_vc_prepare(int64_t vh, const float* feats, int64_t F, int64_t D, dou
     h2d(x, feats, sizeof(float) * (size_t)F * D, s);
     if (pf) h2d(pf, pitchf, sizeof(float) * (size_t)2 * F, s);
     v.prepare(x, (int)F, (int)D, index_rate, pf, protect, o);
+    v.close_span();
     d2h(out, o, sizeof(float) * (size_t)2 * F * D, s);
     v.eng->sync();
     v.collect_timing();
@@ -304,6 +307,7 @@ int32_t rvc_vc_prepare_dev(int64_t vh, int64_t feats, int64_t F, int64_t D, doub
     float* o = e.fptr(out, 2 * F * D, "prepare out");
     RVC_CHECK(o != x, "prepare: out must not alias feats");
     v.prepare(x, (int)F, (int)D, index_rate, pf, protect, o);
+    v.close_span();
     e.sync();
     v.collect_timing();
   });
@@ -322,6 +326,7 @@ int32_t rvc_vc_change_rms(int64_t vh, const float* data1, int64_t n1, int64_t sr
     h2d(a, data1, sizeof(float) * (size_t)n1, s);
     h2d(b, data2, sizeof(float) * (size_t)n2, s);
     v.change_rms(a, n1, (int)sr1, b, n2, (int)sr2, rate, o);
+    v.close_span();
     d2h(out, o, sizeof(float) * (size_t)n2, s);
     v.eng->sync();
     v.collect_timing();
@@ -338,6 +343,7 @@ int32_t rvc_vc_change_rms_dev(int64_t vh, int64_t data1, int64_t n1, int64_t sr1
     const float* b = e.fptr(data2, n2, "change_rms data2");
     float* o = e.fptr(out, n2, "change_rms out");
     v.change_rms(a, n1, (int)sr1, b, n2, (int)sr2, rate, o);
+    v.close_span();
     e.sync();
     v.collect_timing();
   });
@@ -352,6 +358,7 @@ int32_t rvc_vc_to_int16(int64_t vh, const float* x, int64_t n, int16_t* out) {
     short* o = reinterpret_cast<short*>(v.buf("out_i16", (size_t)(n + 1) / 2));
     h2d(a, x, sizeof(float) * (size_t)n, s);
     v.to_int16(a, n, o);
+    v.close_span();
     d2h(out, o, sizeof(short) * (size_t)n, s);
     v.eng->sync();
     v.collect_timing();
@@ -367,6 +374,7 @@ int32_t rvc_vc_to_int16_dev(int64_t vh, int64_t x, int64_t n, int64_t out) {
     DevBuf& ob = e.get(out);
     RVC_CHECK(ob.bytes >= (size_t)n * 2, "to_int16 out: buffer too small (int16 [n])");
     v.to_int16(a, n, static_cast<short*>(ob.ptr));
+    v.close_span();
     e.sync();
     v.collect_timing();
   });

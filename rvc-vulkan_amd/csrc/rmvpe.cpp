@@ -592,6 +592,7 @@ int32_t rvc_rmvpe_infer(int64_t hh, const float* x, int64_t T, double thred, flo
     float* df = s.buf("out_f0", (size_t)F);
     RVC_HIP(hipMemcpyAsync(dx, x, sizeof(float) * T, hipMemcpyHostToDevice, st));
     s.infer(dx, T, (float)thred, df);
+    s.close_span();
     RVC_HIP(hipMemcpyAsync(f0, df, sizeof(float) * F, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
     s.check_gru();
@@ -606,6 +607,7 @@ int32_t rvc_rmvpe_infer_dev(int64_t hh, int64_t x, int64_t T, double thred, int6
     const float* xp = e.fptr(x, T, "rmvpe audio");
     float* fp = e.fptr(f0, Rmvpe::frames(T), "rmvpe f0");
     s.infer(xp, T, (float)thred, fp);
+    s.close_span();
     e.sync();
     s.check_gru();
     s.collect_timing();

@@ -28,7 +28,19 @@ struct SessionBase {
   struct Ev {
     hipEvent_t a, b;
     double flops, bytes;
+    long long n;  // launches between the two events
   };
+  // Consecutive timed launches on one stream share one event pair: an event
+  // record between two kernels costs several microseconds of idle GPU, which
+  // would otherwise land inside the very region being timed.
+  struct Span {
+    bool open = false;
+    hipEvent_t a{};
+    hipStream_t st{};
+    double flops = 0, bytes = 0;
+    long long n = 0;
+  } span;
+  int run_depth = 0;
   std::vector<Ev> pending;
   std::vector<hipEvent_t> pool;
   double t_ms = 0, t_flops = 0, t_bytes = 0;
@@ -38,6 +50,7 @@ struct SessionBase {
     if (eng && eng->stream) (void)hipStreamSynchronize(eng->stream);
     for (void* p : owned) (void)hipFree(p);
     for (auto& kv : ws) (void)hipFree(kv.second.first);
+    if (span.open) pool.push_back(span.a);
     for (auto& e : pending) pool.push_back(e.a), pool.push_back(e.b);
     for (hipEvent_t e : pool) (void)hipEventDestroy(e);
   }
@@ -163,35 +176,68 @@ struct SessionBase {
     RVC_HIP(hipEventCreate(&e));
     return e;
   }
-  // Run fn (launches on stream st, the engine stream by default); when the
-  // tag is timed, bracket it with events on that stream.
+  // Run fn (launches on stream st, the engine stream by default).  A timed
+  // tag joins the open span on that stream (or opens one with a start
+  // event); an untimed launch, a launch on another stream or close_span()
+  // ends the span with its end event.  Launches nested inside fn are part of
+  // the outer one.
   template <class Fn>
   void run(const char* t, double flops, double bytes, Fn&& fn, hipStream_t st = nullptr) {
-    if (!timed(t)) {
+    if (run_depth > 0) {
       fn();
       return;
     }
     if (!st) st = eng->stream;
-    Ev e{ev(), ev(), flops, bytes};
-    RVC_HIP(hipEventRecord(e.a, st));
+    if (!timed(t)) {
+      close_span();
+      ++run_depth;
+      fn();
+      --run_depth;
+      return;
+    }
+    if (span.open && span.st != st) close_span();
+    if (!span.open) {
+      span = Span{};
+      span.open = true;
+      span.a = ev();
+      span.st = st;
+      RVC_HIP(hipEventRecord(span.a, st));
+    }
+    ++run_depth;
     fn();
-    RVC_HIP(hipEventRecord(e.b, st));
-    pending.push_back(e);
+    --run_depth;
+    span.flops += flops;
+    span.bytes += bytes;
+    ++span.n;
+  }
+  // Ends the open span; sessions call it after their last launch and before
+  // the copies and synchronisation that end a call.
+  void close_span() {
+    if (!span.open) return;
+    span.open = false;
+    hipEvent_t b = ev();
+    RVC_HIP(hipEventRecord(b, span.st));
+    pending.push_back(Ev{span.a, b, span.flops, span.bytes, span.n});
   }
   void collect_timing() {
+    // Only a call that ended early (an error) leaves a span open here; its
+    // end event then lands after the synchronisation.
+    close_span();
     for (auto& e : pending) {
       float ms = 0;
       RVC_HIP(hipEventElapsedTime(&ms, e.a, e.b));
       t_ms += ms;
       t_flops += e.flops;
       t_bytes += e.bytes;
-      ++t_n;
+      t_n += e.n;
       pool.push_back(e.a);
       pool.push_back(e.b);
     }
     pending.clear();
   }
   void set_timing(const char* t) {
+    if (span.open) pool.push_back(span.a);
+    span.open = false;
     tag = t ? t : "";
     t_ms = t_flops = t_bytes = 0;
     t_n = 0;

@@ -696,6 +696,7 @@ int32_t rvc_synth_infer_dev(int64_t sh, int64_t phone, int64_t pitch, int64_t ns
     s.decode_prep(g, f0, nsp, (int)B, (int)P);
     const float* z = s.enc_flow(ph, static_cast<const long long*>(pb.ptr), nzp, (int)B, (int)P, g);
     s.decode_main(z, (long long)s.H * P, (int)B, (int)P, wv);
+    s.close_span();
     e.sync();
     s.collect_timing();
   });
@@ -730,6 +731,7 @@ int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, co
     s.decode_prep(g, d_f0, d_ns, (int)B, (int)P);
     const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g);
     s.decode_main(z, (long long)s.H * P, (int)B, (int)P, d_w);
+    s.close_span();
     RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
     s.collect_timing();
@@ -748,6 +750,7 @@ int32_t rvc_synth_decode_dev(int64_t sh, int64_t z, int64_t f0, int64_t g, int64
     const float* np_ = e.fptr(ns, B * P * s.upp, "decode ns");
     float* wv = e.fptr(wave, B * P * s.upp, "decode wave");
     s.decode(zp, (long long)s.H * P, gp, fp, np_, (int)B, (int)P, wv);
+    s.close_span();
     e.sync();
     s.collect_timing();
   });
@@ -771,6 +774,7 @@ int32_t rvc_synth_decode(int64_t sh, const float* z, const float* f0, const floa
     RVC_HIP(hipMemcpyAsync(d_g, g, sizeof(float) * B * s.gin, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
     s.decode(d_z, (long long)s.H * P, d_g, d_f0, d_ns, (int)B, (int)P, d_w);
+    s.close_span();
     RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
     s.collect_timing();
