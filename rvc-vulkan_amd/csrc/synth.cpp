@@ -376,7 +376,6 @@ struct Synth : SessionBase {
     float* skip = buf("fskip", (size_t)B * HP);
     float* xi = buf("fxi", (size_t)B * 2 * HP);
     float* acts = buf("facts", (size_t)B * HP);
-    float* rs = buf("frs", (size_t)B * 2 * HP);
     float* m = buf("fm", (size_t)B * half * P);
     const float* src = zp;
     int k = 0;
@@ -387,9 +386,9 @@ struct Synth : SessionBase {
       conv("flow.pre", c1x1(dst, HP, L.pre_w, L.pre_b, h, B, half, H, P));
       launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s);
       for (int i = 0; i < kWnLayers; ++i) {
-        // in-layer conv + gate, and res/skip conv + update: fused into the
-        // split-K reduce when the conv takes the split path (it does at
-        // P <= ~2000), as separate elementwise launches otherwise
+        // in-layer conv + gate: fused into the split-K reduce when the conv
+        // takes the split path (it does at P <= ~2000), a separate
+        // elementwise launch otherwise
         ConvLaunch ci = cargs_same(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
                                    (kWnKernel - 1) / 2);
         if (conv1d_mfma_split_floats(ci) > 0) {
@@ -405,19 +404,24 @@ struct Synth : SessionBase {
           conv("flow.in", ci);
           launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
         }
-        ConvLaunch cr = c1x1(acts, HP, L.rs_w[i], L.rs_b[i], rs, B, H, L.rs_out[i], P);
-        if (conv1d_mfma_split_floats(cr) > 0) {
-          cr.post = POST_WN_UPDATE;
-          cr.post_h = h;
-          cr.post_skip = skip;
-          cr.post_H = H;
-          cr.post_first = i == 0;
-          cr.post_last = i == kWnLayers - 1;
-          conv("flow.rs", cr);
-        } else {
-          conv("flow.rs", cr);
-          launch_wn_update(h, skip, rs, B, H, P, i == 0, i == kWnLayers - 1, s);
+        // res/skip conv as one launch of two output groups over the same
+        // input: rows [0, H) accumulate into h (h += rs[:H]), rows [H, 2H)
+        // into skip (skip = rs[H:] on the first layer); the last layer has
+        // only the skip rows.  Each output adds (conv + bias), the
+        // reference's order.
+        const bool has_h = i + 1 < kWnLayers;
+        ConvLaunch cr = c1x1(acts, HP, L.rs_w[i], L.rs_b[i], has_h ? h : skip, B, H, H, P);
+        cr.w_ld = packed_ld(L.rs_out[i]);
+        cr.g[0].combine = has_h || i > 0 ? COMB_ADD : COMB_STORE;
+        if (has_h) {
+          cr.n_groups = 2;
+          cr.g[1] = cr.g[0];
+          cr.g[1].w = L.rs_w[i] + H;
+          cr.g[1].bias = L.rs_b[i] + H;
+          cr.g[1].out = skip;
+          cr.g[1].combine = i == 0 ? COMB_STORE : COMB_ADD;
         }
+        conv("flow.rs", cr);
       }
       conv("flow.post", c1x1(skip, HP, L.post_w, L.post_b, m, B, H, half, P));
       launch_sub_inplace_strided(dst + (long long)half * P, HP, m, (long long)half * P, B, half, P, s);
