@@ -71,10 +71,11 @@ def test_conv1d_resblock_shapes(ops, C, L, k, d):
 
 
 @pytest.mark.parametrize("C,L,k,d", [(256, 30000, 3, 1), (128, 120000, 3, 3), (64, 240000, 3, 1),
-                                     (32, 500000, 3, 5)])
+                                     (32, 500000, 3, 5), (128, 240000, 3, 5)])
 def test_conv1d_persistent_tiles(ops, C, L, k, d):
-    """Grids large enough for the persistent MFMA kernel (32 x 256, 64 x 256
-    and 32 x 512 tiles, buffer-resource staging with out-of-range padding)."""
+    """Grids large enough for the persistent MFMA kernel (32 x 256, 64 x 256,
+    128 x 256 and 32 x 512 tiles, buffer-resource staging with out-of-range
+    padding)."""
     print(f"persistent conv C={C} L={L} k={k} d={d}", flush=True)
     rng = np.random.default_rng(C + L)
     x = _r(rng, 1, C, L)
@@ -83,6 +84,26 @@ def test_conv1d_persistent_tiles(ops, C, L, k, d):
     pad = (k * d - d) // 2
     got = ops.conv1d(x, w, b, padding=pad, dilation=d)
     assert rel_l2(got, nn.conv1d(x, w, b, padding=pad, dilation=d)) < TOL
+
+
+def test_conv1d_persistent_widest_halo(ops):
+    """The persistent 64 x 256 tile at decoder stage 1's widest ResBlock conv
+    (C = 128, k = 11, d = 5: a 306-sample staged row per channel), checked
+    against torch's fp32 CPU conv1d (the numpy oracle needs about a minute
+    for these 86 GFLOP)."""
+    import torch
+
+    C, L, k, d = 128, 240000, 11, 5
+    print(f"persistent conv C={C} L={L} k={k} d={d}", flush=True)
+    rng = np.random.default_rng(17)
+    x = _r(rng, 1, C, L)
+    w = _r(rng, C, C, k, scale=1.0 / np.sqrt(C * k))
+    b = _r(rng, C, scale=0.1)
+    pad = (k * d - d) // 2
+    got = ops.conv1d(x, w, b, padding=pad, dilation=d)
+    want = torch.nn.functional.conv1d(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(b), padding=pad,
+                                      dilation=d).numpy()
+    assert rel_l2(got, want) < TOL
 
 
 @pytest.mark.parametrize("C_in,C_out,L,K", [(192, 512, 200, 7), (192, 768, 300, 3), (768, 192, 300, 3),
