@@ -73,7 +73,8 @@ __global__ __launch_bounds__(256) void conv1d_direct_kernel(DirectConvArgs a) {
 // Thread t computes output t, so a wave reads 64 neighbouring LDS words per
 // tap; the small tile keeps several workgroups per CU in flight to hide the
 // load latency of each chunk.  Per output the sum runs channel-major, taps
-// inner, as in conv1d_direct_kernel.
+// inner, as in conv1d_direct_kernel.  With x2 / x3 the staged sample is the
+// decoder's three-ResBlock average of the three inputs.
 constexpr int kRowOut = 256, kRowCh = 8, kRowHaloMax = 128;
 __global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
   __shared__ float rows[kRowCh][kRowOut + kRowHaloMax];
@@ -83,15 +84,23 @@ __global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
   const int tid = threadIdx.x;
   const int W = kRowOut + (a.K - 1) * a.dil;  // launcher: (K - 1) * dil <= kRowHaloMax
   const float* xb = a.x + (long long)b * a.xb;
+  const float* xb2 = a.x2 ? a.x2 + (long long)b * a.xb : nullptr;
+  const float* xb3 = a.x2 ? a.x3 + (long long)b * a.xb : nullptr;
   const long long tb = (long long)i0 + a.in_off;
   float acc = 0.f;
   for (int ci0 = 0; ci0 < a.C_in; ci0 += kRowCh) {
     const int nch = min(kRowCh, a.C_in - ci0);
     for (int r = 0; r < nch; ++r) {
-      const float* xr = xb + (long long)(ci0 + r) * a.xc;
+      const long long ro = (long long)(ci0 + r) * a.xc;
       for (int c = tid; c < W; c += 256) {
         const long long t = tb + c;
-        rows[r][c] = (t >= 0 && t < a.L_in) ? act_in(xr[t], a.in_act, a.in_slope) : 0.f;
+        float v = 0.f;
+        if (t >= 0 && t < a.L_in) {
+          v = xb[ro + t];
+          if (xb2) v = ((v + xb2[ro + t]) + xb3[ro + t]) / 3.0f;  // the decoder's ((o1 + o2) + o3) / 3
+          v = act_in(v, a.in_act, a.in_slope);
+        }
+        rows[r][c] = v;
       }
     }
     __syncthreads();
@@ -204,6 +213,8 @@ unsigned grid1d(long long n) { return (unsigned)((n + 255) / 256); }
 void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
   RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.K >= 1 && a.stride >= 1 && a.dil >= 1 && a.B >= 1,
             "conv1d_direct: invalid shape");
+  RVC_CHECK(!a.x2 || (a.x3 && a.C_out < 8 && a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax),
+            "conv1d_direct: a three-input average needs the stride-1 row kernel");
   if (a.n_out <= 0) return;
   if (a.C_out >= 8) {
     dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);

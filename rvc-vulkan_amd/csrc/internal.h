@@ -173,6 +173,9 @@ inline int packed_ld(int c_out) { return (c_out + 3) / 4 * 4; }
 // x[b][ci][i*stride + in_off + k*dil].
 struct DirectConvArgs {
   const float* x; long long xb, xc;
+  // x2, x3 (optional, same layout as x): the input is ((x + x2) + x3) / 3,
+  // formed while staging (stride-1 launches with fewer than 8 outputs only)
+  const float* x2; const float* x3;
   const float* w;  // PyTorch layout [C_out][C_in][K]
   const float* bias;
   float* out; long long ob, oc;

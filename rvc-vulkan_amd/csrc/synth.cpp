@@ -513,6 +513,8 @@ struct Synth : SessionBase {
     static const int ks[3] = {3, 7, 11};
     static const int ds[3] = {1, 3, 5};
     char tg[32];
+    bool fold_avg = false;
+    const float* avg_in[3] = {nullptr, nullptr, nullptr};
     for (int i = 0; i < n_ups; ++i) {
       const int C = chans[i];
       const int Lo = L * rates[i];
@@ -571,7 +573,16 @@ struct Synth : SessionBase {
         conv(tg, c1);
         conv(tg, c2);
       }
-      run("dec.avg", 0.0, 16.0 * B * CL, [&] { launch_avg3(A, T[0], T[1], T[2], B * CL, s); });
+      // the last stage's average is formed by conv_post while it stages its
+      // input (unless the stage outputs are kept)
+      fold_avg = i == n_ups - 1 && !keep_stages;
+      if (fold_avg) {
+        avg_in[0] = T[0];
+        avg_in[1] = T[1];
+        avg_in[2] = T[2];
+      } else {
+        run("dec.avg", 0.0, 16.0 * B * CL, [&] { launch_avg3(A, T[0], T[1], T[2], B * CL, s); });
+      }
       if (keep_stages) {
         float* keep = buf("dec_stage" + std::to_string(i), (size_t)B * CL);
         launch_copy(keep, A, B * CL, s);
@@ -582,6 +593,11 @@ struct Synth : SessionBase {
     }
     DirectConvArgs p{};
     p.x = cur; p.xb = (long long)c_in * L; p.xc = L;
+    if (fold_avg) {
+      p.x = avg_in[0];
+      p.x2 = avg_in[1];
+      p.x3 = avg_in[2];
+    }
     p.w = dpost_w; p.bias = nullptr;
     p.out = wave; p.ob = L; p.oc = L;
     p.C_in = c_in; p.C_out = 1; p.L_in = L; p.n_out = L;
