@@ -260,14 +260,40 @@ int32_t rvc_synth_finalize(int64_t s, int64_t sr, const int64_t* rates, const in
 int32_t rvc_synth_infer(int64_t s, const float* phone, const int64_t* pitch, const float* nsff0,
                         const int64_t* sid, const float* nz, const float* ns, int64_t B, int64_t P,
                         float* wave);
-/* Same with engine buffer ids (inputs already resident; pitch/sid hold int64). */
+/* Same with engine buffer ids (inputs already resident; pitch/sid hold int64).
+ * A pitch or sid id outside [-rows, rows) fails the call (-1, "... out of
+ * range"), as the host path and numpy's take do. */
 int32_t rvc_synth_infer_dev(int64_t s, int64_t phone, int64_t pitch, int64_t nsff0, int64_t sid,
                             int64_t nz, int64_t ns, int64_t B, int64_t P, int64_t wave);
+/* enc_p + flow without the decoder: SynthesizerTrn._full_prep (flow_head = 0)
+ * and the enc_p/flow half of _partial_prep (runtime/models/vits.py:2416-2500):
+ * enc_p over all P frames, z_p = m + exp(logs)*nz*0.66666, the flow over
+ * frames [flow_head, P).  z_out [B,hidden,P-flow_head]; g_out [B,gin]
+ * (nullable); phase_out [B,P] (nullable, needs nsff0 [B,P]) receives
+ * _phase_offsets(nsff0) = fmod(cumsum(fmod(f0/sr*upp + 0.5, 1) - 0.5), 1)
+ * (:2404-2414). */
+int32_t rvc_synth_prep(int64_t s, const float* phone, const int64_t* pitch, const float* nsff0,
+                       const int64_t* sid, const float* nz, int64_t B, int64_t P, int64_t flow_head,
+                       float* z_out, float* g_out, float* phase_out);
+/* SynthesizerTrn._phase_offsets (runtime/models/vits.py:2404-2414) of nsff0
+ * [B,P]: out [B,P] = fmod(cumsum(fmod(f0/sr*upp + 0.5, 1) - 0.5), 1), the
+ * cumulative sum taken sequentially in float32. */
+int32_t rvc_synth_phase_offsets(int64_t s, const float* nsff0, int64_t B, int64_t P, float* out);
 /* Decoder only: z [B,hidden,P], f0 [B,P], g [B,gin], ns [B,P*upp] -> wave [B,P*upp]. */
 int32_t rvc_synth_decode(int64_t s, const float* z, const float* f0, const float* g, const float* ns,
                          int64_t B, int64_t P, float* wave);
 int32_t rvc_synth_decode_dev(int64_t s, int64_t z, int64_t f0, int64_t g, int64_t ns, int64_t B,
                              int64_t P, int64_t wave);
+/* _GeneratorNSF.decode_batch (runtime/models/vits.py:1847-1878): n chunks of
+ * P[i] frames each, z[i] [hidden,P[i]], f0[i] [P[i]], ns[i] [P[i]*upp], off[i]
+ * [P[i]] (the per-frame phase offsets seg_offsets, :1484-1491; off or off[i]
+ * may be null for f0's own cumulative phase), one speaker g [gin] (null: no
+ * speaker term) -> wave[i] [P[i]*upp].  Chunks of equal length run as one
+ * batch and the batches follow each other on one stream; each result equals
+ * that chunk's own decode bit for bit. */
+int32_t rvc_synth_decode_chunks(int64_t s, int64_t n, const float* const* z, const float* const* f0,
+                                const float* const* ns, const float* const* off, const int64_t* P,
+                                const float* g, float* const* wave);
 /* Copy a named intermediate of the last run to the host (n floats): "enc_in",
  * "enc_out", "stats", "z_p", "z", "g", "har", "dec_pre", "dec_stage0".."dec_stage3". */
 int32_t rvc_synth_read(int64_t s, const char* name, float* dst, int64_t n);

@@ -34,6 +34,10 @@ __all__ = [
 ]
 
 _UPP_48K = 480
+# partial synthesis context (runtime/models/vits.py:141-152): decoder frames
+# either side of the target segment, and the flow's receptive field
+DEC_PAD = 16
+FLOW_PAD = 24
 
 
 class VitsConfig:
@@ -355,16 +359,104 @@ class Synthesizer:
         """``emb_g[sid]`` -> [1,gin,1] (:2268-2270)."""
         return nn.embedding(sid, self.w["emb_g.weight"])[0].reshape(1, -1, 1)
 
-    def make_noise(self, P, seed):
-        """nz [1,h,P] then ns [1,P*upp,1] from one RandomState (:2337-2350)."""
-        rng = np.random.RandomState(seed)
+    def make_noise(self, P, seed, fixed_seed=""):
+        """nz [1,h,P] then ns [1,P*upp,1] from one RandomState (:2337-2350);
+        ``fixed_seed`` (the RVC_FIXED_SEED text) replaces ``seed=None``."""
+        if seed is None and fixed_seed:
+            seed = int(fixed_seed)
+        rng = np.random.RandomState(seed) if seed is not None else np.random.RandomState()
         nz = rng.standard_normal((1, self.cfg.hidden, P)).astype(np.float32)
         ns = rng.standard_normal((1, P * self.cfg.upp, 1)).astype(np.float32)
         return nz, ns
 
-    def infer(self, phone, pitch, nsff0, sid, seed):
+    def infer(self, phone, pitch, nsff0, sid, seed, skip_head=None, return_length=None):
+        """``infer`` (:2352-2402): full synthesis, or the partial synthesis of
+        frames [skip_head, skip_head + return_length)."""
         nz, ns = self.make_noise(phone.shape[1], seed)
-        return self.infer_controlled(phone, pitch, nsff0, sid, nz, ns)
+        if skip_head is None or return_length is None:
+            return self.infer_controlled(phone, pitch, nsff0, sid, nz, ns)
+        head, length = self._check_part(phone.shape[1], skip_head, return_length)
+        p = self.partial_prep(phone, pitch, nsff0, sid, nz, ns, head, length)
+        o = self.dec.forward(p["z_seg"], p["nsff0_seg"], p["g"], p["ns_seg"], seg_offsets=p["off"])
+        return o[:, :, p["s0"]:p["s0"] + p["n_out"]]
+
+    @staticmethod
+    def _check_part(P, skip_head, return_length):
+        head, length = int(skip_head), int(return_length)
+        if head < 0 or head >= P or length <= 0 or head + length > P:
+            raise ValueError(f"skip_head/return_length out of range: P={P}, head={head}, length={length}")
+        return head, length
+
+    def phase_offsets(self, nsff0):
+        """``_phase_offsets`` (:2404-2414): the full run's per-frame
+        fmod-cumsum phase [1,P,1]."""
+        cfg = self.cfg
+        f0r = nsff0[:, None].transpose(0, 2, 1)
+        rad = f0r / cfg.sr * np.arange(1, cfg.upp + 1, dtype=np.float32)[None, None, :]
+        rad2 = np.fmod(rad[..., -1:] + 0.5, 1.0) - 0.5
+        return np.fmod(np.cumsum(rad2, axis=1), 1.0)
+
+    def _enc_stats(self, phone, pitch, sid):
+        cfg = self.cfg
+        g = self.resolve_g(sid)
+        x = self.enc_p.embed(phone, pitch)
+        x = x * math.sqrt(cfg.hidden)
+        x = nn.leaky_relu(x, 0.1)
+        x_mask = np.ones((1, 1, phone.shape[1]), dtype=np.float32)
+        m, logs = self.enc_p.stats(self.enc_p.encode(x, x_mask))
+        return g, m * x_mask, logs * x_mask, x_mask
+
+    def full_prep(self, phone, pitch, nsff0, sid, nz, ns):
+        """``_full_prep``: the decoder inputs of ``infer_controlled``."""
+        z, g = self.enc_flow(phone, pitch, sid, nz)
+        P = phone.shape[1]
+        return {"z_seg": z, "nsff0_seg": nsff0, "ns_seg": ns, "off": None, "g": g,
+                "s0": 0, "n_out": P * self.cfg.upp}
+
+    def partial_prep(self, phone, pitch, nsff0, sid, nz, ns, head, length):
+        """``_partial_prep`` (:2416-2476): enc_p over every frame, the flow
+        from ``flow_head = max(head - 24 - 16, 0)``, the decoder segment
+        [zs, ze) = [head - 16, head + length + 16] clipped to [0, P), and the
+        segment's phase offsets taken from the full run's fmod-cumsum."""
+        upp = self.cfg.upp
+        P = phone.shape[1]
+        g, m, logs, x_mask = self._enc_stats(phone, pitch, sid)
+        flow_head = max(head - FLOW_PAD - DEC_PAD, 0)
+        z_p = (m[:, :, flow_head:] + np.exp(logs[:, :, flow_head:]) * nz[:, :, flow_head:] * 0.66666) \
+            * x_mask[:, :, flow_head:]
+        z = self.flow.reverse(z_p, x_mask[:, :, flow_head:], g)
+        zs = max(head - DEC_PAD, 0)
+        ze = min(P, head + length + DEC_PAD)
+        z_seg = z[:, :, zs - flow_head:ze - flow_head]
+        rad_acc = self.phase_offsets(nsff0)
+        n_seg = ze - zs
+        if zs == 0:
+            off = np.zeros((1, n_seg, 1), dtype=np.float32)
+            if n_seg > 1:
+                off[:, 1:, :] = rad_acc[:, :n_seg - 1, :]
+        else:
+            off = rad_acc[:, zs - 1:zs - 1 + n_seg, :]
+        return {"z_seg": z_seg * x_mask[:, :, zs:ze], "nsff0_seg": nsff0[:, zs:ze],
+                "ns_seg": ns[:, zs * upp:ze * upp, :], "off": off, "g": g,
+                "s0": (head - zs) * upp, "n_out": length * upp}
+
+    def prep_dec(self, phone, pitch, nsff0, sid, seed, skip_head=None, return_length=None):
+        """``prep_dec`` (:2478-2500)."""
+        nz, ns = self.make_noise(phone.shape[1], seed)
+        if skip_head is None or return_length is None:
+            return self.full_prep(phone, pitch, nsff0, sid, nz, ns)
+        head, length = self._check_part(phone.shape[1], skip_head, return_length)
+        return self.partial_prep(phone, pitch, nsff0, sid, nz, ns, head, length)
+
+    def decode_batch(self, preps):
+        """``decode_batch(preps)`` (:2502-2522): every chunk's target segment,
+        the speaker of the first prep for all of them."""
+        if not preps:
+            return []
+        outs = self.dec.decode_batch([p["z_seg"] for p in preps], preps[0]["g"],
+                                     [p["nsff0_seg"] for p in preps], [p["ns_seg"] for p in preps],
+                                     [p["off"] for p in preps])
+        return [o[:, :, p["s0"]:p["s0"] + p["n_out"]] for o, p in zip(outs, preps)]
 
     def enc_flow(self, phone, pitch, sid, nz):
         """Steps 1-7 of ``infer_controlled``: returns (z, g) fed to the decoder."""

@@ -319,9 +319,12 @@ void launch_dt(const float* qkv, const float* emb_k, const float* emb_v, float* 
 
 }  // namespace
 
-int relpos_attention_splits(int B, int H, int P) {
+// The key-split count depends on (H, P) only, never on B: the merge order of the
+// split partial sums is part of the result's rounding, so a batched call must use
+// the split a single chunk would, or batch != per-chunk bit for bit.
+int relpos_attention_splits(int /*B*/, int H, int P) {
   const int ntile = (P + 31) / 32;
-  const int blocks = ((P + 31) / 32) * H * B;
+  const int blocks = ((P + 31) / 32) * H;
   int ks = (256 + blocks - 1) / blocks;
   ks = std::min(ks, std::max(1, ntile / AWAVES));
   return std::max(ks, 1);

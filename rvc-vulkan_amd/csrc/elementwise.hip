@@ -111,14 +111,18 @@ __global__ void flip_kernel(const float* src, float* dst, int C, long long L, lo
   }
 }
 
+// An id outside [-rows, rows) (numpy's take would raise) sets bit 0 of *err
+// for the host to report; the read itself is clamped so it stays in bounds.
 __global__ void embed_combine_kernel(const float* E, const long long* pitch, const float* table, float* x,
-                                     int C, int P, int rows, float scale, float slope, long long n) {
+                                     int C, int P, int rows, float scale, float slope, long long n,
+                                     unsigned* err) {
   GRID_STRIDE(e, n) {
     const int t = (int)(e % P);
     const long long bc = e / P;
     const int c = (int)(bc % C);
     const long long b = bc / C;
     long long id = pitch[b * P + t];
+    if ((id < -rows || id >= rows) && err) atomicOr(err, 1u);
     if (id < 0) id += rows;
     id = id < 0 ? 0 : (id >= rows ? rows - 1 : id);
     float v = E[e] + table[id * C + c];
@@ -202,12 +206,14 @@ __global__ void sub_strided_kernel(float* x1, long long x1b, const float* m, lon
   }
 }
 
+// out-of-range ids set bit 1 of *err (reads clamped, as above)
 __global__ void gather_rows_i64_kernel(const long long* ids, const float* table, float* out, int rows,
-                                       int dim, long long n) {
+                                       int dim, long long n, unsigned* err) {
   GRID_STRIDE(e, n) {
     const long long b = e / dim;
     const int c = (int)(e - b * dim);
     long long id = ids[b];
+    if ((id < -rows || id >= rows) && err) atomicOr(err, 2u);
     if (id < 0) id += rows;
     id = id < 0 ? 0 : (id >= rows ? rows - 1 : id);
     out[e] = table[id * dim + c];
@@ -237,8 +243,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* W, const float* 
 // sequential float32 recurrence (numpy's cumsum order): after the workgroup
 // has staged rad2 in LDS, one thread runs the additions alone and the fmod
 // of every prefix is taken in parallel afterwards.
-__global__ __launch_bounds__(256) void sine_phase_kernel(const float* f0, float* acc, int P, int upp,
-                                                         float sr) {
+// Per-frame phase of the NSF source.  rad_acc[p] = fmod(sum_{q<=p} r2[q], 1)
+// with r2[q] = fmod(f0[q]/sr*upp + 0.5, 1) - 0.5, the sum taken sequentially
+// in float32 (numpy's cumsum order), is the reference's _phase_offsets.
+// out[p + shift] = rad_acc[p]: shift 0 writes rad_acc itself; shift 1 writes
+// the offset each frame's phase adds (0 for frame 0, rad_acc[p-1] after it),
+// the form the har kernel reads.
+__global__ __launch_bounds__(256) void sine_phase_kernel(const float* f0, float* out, int P, int upp,
+                                                         float sr, int shift) {
   extern __shared__ float r2[];
   const int b = blockIdx.x;
   const float* fb = f0 + (long long)b * P;
@@ -255,13 +267,17 @@ __global__ __launch_bounds__(256) void sine_phase_kernel(const float* f0, float*
     }
   }
   __syncthreads();
-  float* ab = acc + (long long)b * P;
-  for (int p = threadIdx.x; p < P; p += blockDim.x) ab[p] = fmodf(r2[p], 1.0f);
+  float* ob = out + (long long)b * P;
+  for (int p = threadIdx.x; p + shift < P; p += blockDim.x) ob[p + shift] = fmodf(r2[p], 1.0f);
+  if (shift && threadIdx.x == 0) ob[0] = 0.f;
 }
 
 // har[b][p*upp+u] = tanh(w * (0.1*sin(2pi*rad)*uv + amp*ns) + b) with
-// rad = (f0[p]/sr)*(u+1) + acc[p-1]   (float32, numpy's evaluation order)
-__global__ void sine_har_kernel(const float* f0, const float* ns, const float* acc, float* har, int P,
+// rad = (f0[p]/sr)*(u+1) + off[p]   (float32, numpy's evaluation order).
+// off[p] is the frame's whole phase offset: rad_acc[p-1] (0 at p = 0) for a
+// full synthesis -- adding 0.0 to frame 0 leaves it bit-identical -- or the
+// caller's seg_offsets for a segment (runtime/models/vits.py:1484-1491).
+__global__ void sine_har_kernel(const float* f0, const float* ns, const float* off, float* har, int P,
                                 int upp, float sr, float w_lin, float b_lin, long long n) {
   const float two_pi = 6.2831855f;  // float32(2*pi), as numpy rounds the python scalar
   GRID_STRIDE(e, n) {
@@ -271,8 +287,7 @@ __global__ void sine_har_kernel(const float* f0, const float* ns, const float* a
     const int p = (int)(j / upp);
     const int u = (int)(j - (long long)p * upp);
     const float f = f0[b * P + p];
-    float rad = (f / sr) * (float)(u + 1);
-    if (p > 0) rad = rad + acc[b * P + p - 1];
+    const float rad = (f / sr) * (float)(u + 1) + off[b * P + p];
     const float sine = sinf(two_pi * rad) * 0.1f;
     const float uv = f > 0.f ? 1.f : 0.f;
     const float amp = uv * 0.003f + ((1.f - uv) * 0.1f) / 3.f;
@@ -364,11 +379,11 @@ void launch_flip_channels(const float* src, float* dst, int B, int C, int L, hip
   check_launch("flip_channels");
 }
 void launch_embed_combine(const float* E, const long long* pitch, const float* table, int rows, float* x,
-                          int B, int C, int P, float scale, float slope, hipStream_t s) {
+                          int B, int C, int P, float scale, float slope, unsigned* err, hipStream_t s) {
   const long long n = (long long)B * C * P;
   if (n <= 0) return;
   hipLaunchKernelGGL(embed_combine_kernel, dim3(capped_grid(n)), dim3(256), 0, s, E, pitch, table, x, C,
-                     P, rows, scale, slope, n);
+                     P, rows, scale, slope, n, err);
   check_launch("embed_combine");
 }
 void launch_wn_gate(const float* XI, long long xib, const float* g, long long gb, float* acts, int B,
@@ -406,11 +421,11 @@ void launch_sub_inplace_strided(float* x1, long long x1b, const float* m, long l
   check_launch("sub_inplace");
 }
 void launch_gather_rows_i64(const long long* ids, const float* table, float* out, int B, int rows, int dim,
-                            hipStream_t s) {
+                            unsigned* err, hipStream_t s) {
   const long long n = (long long)B * dim;
   if (n <= 0) return;
   hipLaunchKernelGGL(gather_rows_i64_kernel, dim3(capped_grid(n)), dim3(256), 0, s, ids, table, out, rows, dim,
-                     n);
+                     n, err);
   check_launch("gather_rows");
 }
 void launch_gemv(const float* W, const float* bias, const float* g, long long gb, float* out, long long ob,
@@ -421,15 +436,19 @@ void launch_gemv(const float* W, const float* bias, const float* g, long long gb
                      C_in, n);
   check_launch("gemv");
 }
-void launch_sine_source(const float* f0, const float* ns, float* har, float* acc, int B, int P, int upp,
-                        float sr, float w_lin, float b_lin, hipStream_t s) {
+void launch_sine_phase(const float* f0, float* out, int B, int P, int upp, float sr, int shift, hipStream_t s) {
   if ((long long)B * P == 0) return;
   RVC_CHECK((size_t)P * sizeof(float) <= 65536, "sine_source: too many frames per chunk (max 16384)");
-  hipLaunchKernelGGL(sine_phase_kernel, dim3(B), dim3(256), P * sizeof(float), s, f0, acc, P, upp, sr);
+  hipLaunchKernelGGL(sine_phase_kernel, dim3(B), dim3(256), P * sizeof(float), s, f0, out, P, upp, sr, shift);
   check_launch("sine_phase");
+}
+void launch_sine_source(const float* f0, const float* ns, float* har, float* off, const float* seg_off, int B, int P,
+                        int upp, float sr, float w_lin, float b_lin, hipStream_t s) {
+  if ((long long)B * P == 0) return;
+  if (!seg_off) launch_sine_phase(f0, off, B, P, upp, sr, 1, s);
   const long long n = (long long)B * P * upp;
-  hipLaunchKernelGGL(sine_har_kernel, dim3(capped_grid(n)), dim3(256), 0, s, f0, ns, acc, har, P, upp, sr,
-                     w_lin, b_lin, n);
+  hipLaunchKernelGGL(sine_har_kernel, dim3(capped_grid(n)), dim3(256), 0, s, f0, ns, seg_off ? seg_off : off, har, P,
+                     upp, sr, w_lin, b_lin, n);
   check_launch("sine_har");
 }
 

@@ -254,9 +254,10 @@ void launch_embed_i32(const int* ids, const float* table, float* out, long long 
 void launch_transpose(const float* src, float* out, int B, int C, int P, float scale, hipStream_t s);
 // dst[b][c][t] = src[b][C-1-c][t]
 void launch_flip_channels(const float* src, float* dst, int B, int C, int L, hipStream_t s);
-// x[b][c][t] = lrelu((E[b][c][t] + table[pitch[b][t]][c]) * scale, slope)
+// x[b][c][t] = lrelu((E[b][c][t] + table[pitch[b][t]][c]) * scale, slope); an id
+// outside [-rows, rows) sets bit 0 of *err (nullable) and reads a clamped row
 void launch_embed_combine(const float* E, const long long* pitch, const float* table, int rows, float* x,
-                          int B, int C, int P, float scale, float slope, hipStream_t s);
+                          int B, int C, int P, float scale, float slope, unsigned* err, hipStream_t s);
 // acts[b][c][t] = tanh(a[c] + g[c]) * sigmoid(a[H+c] + g[H+c]), a = XI[b], g per batch [2H]
 void launch_wn_gate(const float* XI, long long xib, const float* g, long long gb, float* acts, int B,
                     int H, int L, hipStream_t s);
@@ -271,17 +272,24 @@ void launch_wn_update(float* h, float* skip, const float* rs, int B, int H, int 
 // x1[b][c][t] = x1 - m   (x1 strided inside z)
 void launch_sub_inplace_strided(float* x1, long long x1b, const float* m, long long mb, int B,
                                 int C, int L, hipStream_t s);
-// out[b][:] = table[clamp(ids[b])][:]  (int64 ids, negative wrap)
+// out[b][:] = table[clamp(ids[b])][:]  (int64 ids, negative wrap); an id outside
+// [-rows, rows) sets bit 1 of *err (nullable)
 void launch_gather_rows_i64(const long long* ids, const float* table, float* out, int B, int rows, int dim,
-                            hipStream_t s);
+                            unsigned* err, hipStream_t s);
 // out[b][co] = bias[co] + sum_ci W[co][ci] * g[b][ci]   (1x1 conv on a length-1 signal)
 void launch_gemv(const float* W, const float* bias, const float* g, long long gb, float* out,
                  long long ob, int B, int C_out, int C_in, hipStream_t s);
 
 // ---------------------------------------------------------------- NSF source
-// har[b][p*upp+u] (see kernel docs); acc scratch [B][P]
-void launch_sine_source(const float* f0, const float* ns, float* har, float* acc, int B, int P,
-                        int upp, float sr, float w_lin, float b_lin, hipStream_t s);
+// Per-frame NSF phase of f0 [B][P]: out[b][p + shift] = rad_acc[b][p] (the
+// reference's _phase_offsets for shift 0; for shift 1, out[b][0] = 0 and each
+// frame gets the offset its phase adds).
+void launch_sine_phase(const float* f0, float* out, int B, int P, int upp, float sr, int shift, hipStream_t s);
+// har[b][p*upp+u] (see kernel docs).  seg_off [B][P] (nullable) holds every
+// frame's whole phase offset (the reference's seg_offsets); without it the
+// offsets come from f0's own cumulative phase, computed into off [B][P].
+void launch_sine_source(const float* f0, const float* ns, float* har, float* off, const float* seg_off, int B,
+                        int P, int upp, float sr, float w_lin, float b_lin, hipStream_t s);
 
 // ---------------------------------------------------------------- norms
 // Row-major LayerNorm over the last axis: x[rows][cols].

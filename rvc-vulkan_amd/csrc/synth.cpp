@@ -87,6 +87,32 @@ struct Synth : SessionBase {
     if (forked) (void)hipEventDestroy(forked);
     if (joined) (void)hipEventDestroy(joined);
     if (side) (void)hipStreamDestroy(side);
+    if (errh) (void)hipHostFree(errh);
+  }
+
+  // ---- id validation on the device path ----
+  // The pitch / speaker gathers of a call whose ids live in device memory set
+  // bits of errw for ids outside [-rows, rows); the word is cleared at the
+  // start of the call and copied to pinned host memory before its final
+  // synchronisation, so checking it costs no extra round trip.
+  unsigned* errw = nullptr;
+  unsigned* errh = nullptr;
+  void begin_ids() {
+    if (!errw) {
+      void* p = nullptr;
+      RVC_HIP(hipMalloc(&p, 256));
+      owned.push_back(p);
+      errw = static_cast<unsigned*>(p);
+      RVC_HIP(hipHostMalloc((void**)&errh, sizeof(unsigned), hipHostMallocDefault));
+    }
+    *errh = 0;
+    launch_fill(reinterpret_cast<float*>(errw), 1, 0.f, eng->stream);  // +0.0f is the bit pattern 0
+  }
+  void fetch_ids() { RVC_HIP(hipMemcpyAsync(errh, errw, sizeof(unsigned), hipMemcpyDeviceToHost, eng->stream)); }
+  // after the call's synchronisation
+  void check_ids() const {
+    RVC_CHECK(!(*errh & 1u), "infer: pitch id out of range");
+    RVC_CHECK(!(*errh & 2u), "infer: sid out of range");
   }
 
   // ---- workspace ----
@@ -325,20 +351,24 @@ struct Synth : SessionBase {
   // -------------------------------------------------------------- enc_p + flow
   // g [B][gin] = emb_g(sid)
   void speaker(const long long* sid, int B, float* g) {
-    launch_gather_rows_i64(sid, emb_g, g, B, n_spk, gin, eng->stream);
+    run("enc.glue", 0.0, 8.0 * B + 8.0 * B * gin,
+        [&] { launch_gather_rows_i64(sid, emb_g, g, B, n_spk, gin, errw, eng->stream); });
   }
 
-  // Returns the flow output z [B][H][P] (batch stride H*P); g from speaker().
-  const float* enc_flow(const float* phone, const long long* pitch, const float* nz, int B, int P, const float* g) {
+  // enc_p: embedding, the attention / FFN layers and proj, then
+  // z_p = m + exp(logs) * nz * 0.66666 -> [B][H][P] (batch stride H*P).
+  float* encode(const float* phone, const long long* pitch, const float* nz, int B, int P) {
     hipStream_t s = eng->stream;
     const long long HP = (long long)H * P;
     float* phT = buf("phT", (size_t)B * phone_dim * P);
-    launch_transpose(phone, phT, B, P, phone_dim, 1.0f, s);
+    run("enc.glue", 0.0, 8.0 * B * phone_dim * P, [&] { launch_transpose(phone, phT, B, P, phone_dim, 1.0f, s); });
     float* E = buf("encE", (size_t)B * HP);
     conv("enc.embed", with16(c1x1(phT, (long long)phone_dim * P, emb_phone_w, emb_phone_b, E, B, phone_dim, H, P),
                              emb_phone16));
     float* xin = buf("enc_in", (size_t)B * HP);
-    launch_embed_combine(E, pitch, emb_pitch, pitch_rows, xin, B, H, P, (float)std::sqrt((double)H), 0.1f, s);
+    run("enc.glue", 0.0, 4.0 * B * (3.0 * HP + 2.0 * P), [&] {
+      launch_embed_combine(E, pitch, emb_pitch, pitch_rows, xin, B, H, P, (float)std::sqrt((double)H), 0.1f, errw, s);
+    });
     float* xo = buf("enc_out", (size_t)B * HP);
     float* qkv = buf("qkv", (size_t)B * 3 * HP);
     float* att = buf("att", (size_t)B * HP);
@@ -367,9 +397,15 @@ struct Synth : SessionBase {
     float* st = buf("stats", (size_t)B * 2 * HP);
     conv("enc.proj", with16(c1x1(x, HP, proj_w, proj_b, st, B, H, 2 * H, P), proj16));
     float* zp = buf("z_p", (size_t)B * HP);
-    launch_zp(st, nz, zp, B, H, P, 0.66666f, s);
+    run("enc.glue", 3.0 * B * HP, 16.0 * B * HP, [&] { launch_zp(st, nz, zp, B, H, P, 0.66666f, s); });
+    return zp;
+  }
 
-    // flow.reverse: Flip, RC(6), Flip, RC(4), ... RC(0)
+  // flow.reverse of src [B][H][P] (batch stride H*P): Flip, RC(6), Flip,
+  // RC(4), ... RC(0).  Returns z [B][H][P] in a workspace buffer.
+  const float* flow(const float* src, int B, int P, const float* g) {
+    hipStream_t s = eng->stream;
+    const long long HP = (long long)H * P;
     float* fz[2] = {buf("fz0", (size_t)B * HP), buf("fz1", (size_t)B * HP)};
     float* h = buf("fh", (size_t)B * HP);
     float* gv = buf("fgv", (size_t)B * 2 * H * kWnLayers);
@@ -377,14 +413,14 @@ struct Synth : SessionBase {
     float* xi = buf("fxi", (size_t)B * 2 * HP);
     float* acts = buf("facts", (size_t)B * HP);
     float* m = buf("fm", (size_t)B * half * P);
-    const float* src = zp;
     int k = 0;
     for (int fi = n_flows - 1; fi >= 0; --fi) {
       const FlowL& L = flows[fi];
       float* dst = fz[k];
-      launch_flip_channels(src, dst, B, H, P, s);
+      run("flow.glue", 0.0, 8.0 * B * HP, [&] { launch_flip_channels(src, dst, B, H, P, s); });
       conv("flow.pre", c1x1(dst, HP, L.pre_w, L.pre_b, h, B, half, H, P));
-      launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s);
+      run("flow.glue", 2.0 * B * gin * 2.0 * H * kWnLayers, 4.0 * (B * gin + (double)(gin + 1 + B) * 2 * H * kWnLayers),
+          [&] { launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s); });
       for (int i = 0; i < kWnLayers; ++i) {
         // in-layer conv + gate: fused into the split-K reduce when the conv
         // takes the split path (it does at P <= ~2000), a separate
@@ -402,18 +438,26 @@ struct Synth : SessionBase {
           conv("flow.in", ci);
         } else {
           conv("flow.in", ci);
-          launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
+          run("flow.glue", 0.0, 12.0 * B * HP, [&] {
+            launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
+          });
         }
         // res/skip conv as one launch of two output groups over the same
         // input: rows [0, H) accumulate into h (h += rs[:H]), rows [H, 2H)
         // into skip (skip = rs[H:] on the first layer); the last layer has
-        // only the skip rows.  Each output adds (conv + bias), the
-        // reference's order.
+        // only the skip rows.  An accumulating group starts its accumulators
+        // at (bias + current value) and adds the conv sum to that, i.e.
+        // (b + h) + sum where the reference forms h + (sum + b): the same
+        // terms in another float32 order.
         const bool has_h = i + 1 < kWnLayers;
         ConvLaunch cr = c1x1(acts, HP, L.rs_w[i], L.rs_b[i], has_h ? h : skip, B, H, H, P);
         cr.w_ld = packed_ld(L.rs_out[i]);
         cr.g[0].combine = has_h || i > 0 ? COMB_ADD : COMB_STORE;
         if (has_h) {
+          // group 1 reads its weights at column offset H of rows packed_ld(2H)
+          // wide; with H % 4 == 0 its float4 loads (masked to C_out = H rounded
+          // up to 4) end inside the row
+          RVC_CHECK(H % 4 == 0, "flow: hidden channels must be a multiple of 4");
           cr.n_groups = 2;
           cr.g[1] = cr.g[0];
           cr.g[1].w = L.rs_w[i] + H;
@@ -424,7 +468,8 @@ struct Synth : SessionBase {
         conv("flow.rs", cr);
       }
       conv("flow.post", c1x1(skip, HP, L.post_w, L.post_b, m, B, H, half, P));
-      launch_sub_inplace_strided(dst + (long long)half * P, HP, m, (long long)half * P, B, half, P, s);
+      run("flow.glue", (double)B * half * P, 12.0 * B * half * P,
+          [&] { launch_sub_inplace_strided(dst + (long long)half * P, HP, m, (long long)half * P, B, half, P, s); });
       src = dst;
       z_name = k == 0 ? "fz0" : "fz1";
       k ^= 1;
@@ -432,11 +477,34 @@ struct Synth : SessionBase {
     return src;
   }
 
+  // enc_p + flow over all P frames (infer_controlled's z)
+  const float* enc_flow(const float* phone, const long long* pitch, const float* nz, int B, int P, const float* g) {
+    return flow(encode(phone, pitch, nz, B, P), B, P, g);
+  }
+
+  // enc_p over all P frames, then the flow over frames [flow_head, P) only:
+  // the reference's partial-synthesis preparation (runtime/models/vits.py:
+  // 2416-2476) when flow_head > 0, enc_flow when it is 0.
+  const float* enc_flow_from(const float* phone, const long long* pitch, const float* nz, int B, int P, int flow_head,
+                             const float* g) {
+    float* zp = encode(phone, pitch, nz, B, P);
+    if (flow_head == 0) return flow(zp, B, P, g);
+    const int Pf = P - flow_head;
+    float* crop = buf("z_p_crop", (size_t)B * H * Pf);
+    RVC_HIP(hipMemcpy2DAsync(crop, sizeof(float) * Pf, zp + flow_head, sizeof(float) * P, sizeof(float) * Pf,
+                             (size_t)B * H, hipMemcpyDeviceToDevice, eng->stream));
+    return flow(crop, B, Pf, g);
+  }
+
   // -------------------------------------------------------------- GeneratorNSF
   // Side-stream half of the decoder: the harmonic source, each stage's noise
   // conv (into dN<i>) and cv = cond(g). Ordered after everything already on
   // the engine stream; decode_main() waits for it.
-  void decode_prep(const float* g, const float* f0, const float* ns, int B, int P) {
+  // g [B][gin] with batch stride gb (0: one speaker for every row), or null
+  // for a decoder without the speaker term; seg_off [B][P] (nullable): every
+  // frame's phase offset (the reference's seg_offsets) instead of f0's own
+  // cumulative phase.
+  void decode_prep(const float* g, long long gb, const float* f0, const float* ns, const float* seg_off, int B, int P) {
     // a call that threw between its fork and its join leaves side-stream
     // work behind; finish it before any of its buffers can be reallocated
     if (side) RVC_HIP(hipStreamSynchronize(side));
@@ -460,9 +528,14 @@ struct Synth : SessionBase {
     RVC_HIP(hipEventRecord(forked, eng->stream));
     RVC_HIP(hipStreamWaitEvent(side, forked, 0));
     hipStream_t s = side;
-    run("dec.sine", 20.0 * B * N, 4.0 * B * (2.0 * N + P),
-        [&] { launch_sine_source(f0, ns, har, phase, B, P, upp, (float)sr, w_lin, b_lin, s); }, s);
-    launch_gemv(dcond_w, dcond_b, g, gin, dec_cv, U, B, U, gin, s);
+    run("dec.sine", 20.0 * B * N, 4.0 * B * (2.0 * N + 2.0 * P),
+        [&] { launch_sine_source(f0, ns, har, phase, seg_off, B, P, upp, (float)sr, w_lin, b_lin, s); }, s);
+    if (g) {
+      run("dec.cond", 2.0 * B * U * gin, 4.0 * ((double)B * gin + (double)U * (gin + 1) + (double)B * U),
+          [&] { launch_gemv(dcond_w, dcond_b, g, gb, dec_cv, U, B, U, gin, s); }, s);
+    } else {
+      dec_cv = nullptr;
+    }
     char tg[32];
     long long L = P;
     for (int i = 0; i < n_ups; ++i) {
@@ -484,9 +557,9 @@ struct Synth : SessionBase {
     RVC_HIP(hipEventRecord(joined, side));
   }
 
-  void decode(const float* z, long long zb, const float* g, const float* f0, const float* ns, int B, int P,
-              float* wave) {
-    decode_prep(g, f0, ns, B, P);
+  void decode(const float* z, long long zb, const float* g, long long gb, const float* f0, const float* ns,
+              const float* seg_off, int B, int P, float* wave) {
+    decode_prep(g, gb, f0, ns, seg_off, B, P);
     decode_main(z, zb, B, P, wave);
   }
 
@@ -712,15 +785,26 @@ int32_t rvc_synth_infer_dev(int64_t sh, int64_t phone, int64_t pitch, int64_t ns
     const float* nsp = e.fptr(ns, B * P * s.upp, "infer ns");
     float* wv = e.fptr(wave, B * P * s.upp, "infer wave");
     float* g = s.buf("g", (size_t)B * s.gin);
+    s.begin_ids();
     s.speaker(static_cast<const long long*>(sb.ptr), (int)B, g);
-    s.decode_prep(g, f0, nsp, (int)B, (int)P);
+    s.decode_prep(g, s.gin, f0, nsp, nullptr, (int)B, (int)P);
     const float* z = s.enc_flow(ph, static_cast<const long long*>(pb.ptr), nzp, (int)B, (int)P, g);
     s.decode_main(z, (long long)s.H * P, (int)B, (int)P, wv);
     s.close_span();
+    s.fetch_ids();
     e.sync();
     s.collect_timing();
+    s.check_ids();
   });
 }
+
+namespace {
+void check_ids_host(const Synth& s, const int64_t* pitch, const int64_t* sid, long long B, long long P) {
+  for (long long i = 0; i < B * P; ++i)
+    RVC_CHECK(pitch[i] >= -s.pitch_rows && pitch[i] < s.pitch_rows, "infer: pitch id out of range");
+  for (long long i = 0; i < B; ++i) RVC_CHECK(sid[i] >= -s.n_spk && sid[i] < s.n_spk, "infer: sid out of range");
+}
+}  // namespace
 
 int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, const float* nsff0, const int64_t* sid,
                         const float* nz, const float* ns, int64_t B, int64_t P, float* wave) {
@@ -728,9 +812,7 @@ int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, co
     s.check_ready();
     s.check_BP(B, P);
     RVC_CHECK(phone && pitch && nsff0 && sid && nz && ns && wave, "infer: null pointer");
-    for (long long i = 0; i < B * P; ++i)
-      RVC_CHECK(pitch[i] >= -s.pitch_rows && pitch[i] < s.pitch_rows, "infer: pitch id out of range");
-    for (long long i = 0; i < B; ++i) RVC_CHECK(sid[i] >= -s.n_spk && sid[i] < s.n_spk, "infer: sid out of range");
+    check_ids_host(s, pitch, sid, B, P);
     hipStream_t st = s.eng->stream;
     const long long N = P * s.upp;
     float* d_ph = s.buf("in_phone", (size_t)(B * P * s.phone_dim));
@@ -748,13 +830,67 @@ int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, co
     RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
     float* g = s.buf("g", (size_t)B * s.gin);
     s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
-    s.decode_prep(g, d_f0, d_ns, (int)B, (int)P);
+    s.decode_prep(g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P);
     const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g);
     s.decode_main(z, (long long)s.H * P, (int)B, (int)P, d_w);
     s.close_span();
     RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
     s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_prep(int64_t sh, const float* phone, const int64_t* pitch, const float* nsff0, const int64_t* sid,
+                       const float* nz, int64_t B, int64_t P, int64_t flow_head, float* z_out, float* g_out,
+                       float* phase_out) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    RVC_CHECK(phone && pitch && sid && nz && z_out, "prep: null pointer");
+    RVC_CHECK(flow_head >= 0 && flow_head < P, "prep: flow_head must be in [0, P)");
+    RVC_CHECK(!phase_out || nsff0, "prep: phase offsets need nsff0");
+    check_ids_host(s, pitch, sid, B, P);
+    hipStream_t st = s.eng->stream;
+    const long long Pf = P - flow_head;
+    float* d_ph = s.buf("in_phone", (size_t)(B * P * s.phone_dim));
+    float* d_pitch = s.buf("in_pitch", (size_t)(B * P * 2));
+    float* d_sid = s.buf("in_sid", (size_t)(B * 2));
+    float* d_nz = s.buf("in_nz", (size_t)(B * s.H * P));
+    RVC_HIP(hipMemcpyAsync(d_ph, phone, sizeof(float) * B * P * s.phone_dim, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_pitch, pitch, 8 * B * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_sid, sid, 8 * B, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
+    float* g = s.buf("g", (size_t)B * s.gin);
+    s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
+    const float* z = s.enc_flow_from(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P,
+                                     (int)flow_head, g);
+    if (phase_out) {
+      float* d_f0 = s.buf("in_f0", (size_t)(B * P));
+      float* d_phase = s.buf("prep_phase", (size_t)(B * P));
+      RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+      launch_sine_phase(d_f0, d_phase, (int)B, (int)P, s.upp, (float)s.sr, 0, st);
+      RVC_HIP(hipMemcpyAsync(phase_out, d_phase, sizeof(float) * B * P, hipMemcpyDeviceToHost, st));
+    }
+    s.close_span();
+    RVC_HIP(hipMemcpyAsync(z_out, z, sizeof(float) * B * s.H * Pf, hipMemcpyDeviceToHost, st));
+    if (g_out) RVC_HIP(hipMemcpyAsync(g_out, g, sizeof(float) * B * s.gin, hipMemcpyDeviceToHost, st));
+    RVC_HIP(hipStreamSynchronize(st));
+    s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_phase_offsets(int64_t sh, const float* nsff0, int64_t B, int64_t P, float* out) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    RVC_CHECK(nsff0 && out, "phase_offsets: null pointer");
+    hipStream_t st = s.eng->stream;
+    float* d_f0 = s.buf("in_f0", (size_t)(B * P));
+    float* d_phase = s.buf("prep_phase", (size_t)(B * P));
+    RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+    launch_sine_phase(d_f0, d_phase, (int)B, (int)P, s.upp, (float)s.sr, 0, st);
+    RVC_HIP(hipMemcpyAsync(out, d_phase, sizeof(float) * B * P, hipMemcpyDeviceToHost, st));
+    RVC_HIP(hipStreamSynchronize(st));
   });
 }
 
@@ -769,7 +905,7 @@ int32_t rvc_synth_decode_dev(int64_t sh, int64_t z, int64_t f0, int64_t g, int64
     const float* gp = e.fptr(g, B * s.gin, "decode g");
     const float* np_ = e.fptr(ns, B * P * s.upp, "decode ns");
     float* wv = e.fptr(wave, B * P * s.upp, "decode wave");
-    s.decode(zp, (long long)s.H * P, gp, fp, np_, (int)B, (int)P, wv);
+    s.decode(zp, (long long)s.H * P, gp, s.gin, fp, np_, nullptr, (int)B, (int)P, wv);
     s.close_span();
     e.sync();
     s.collect_timing();
@@ -793,9 +929,78 @@ int32_t rvc_synth_decode(int64_t sh, const float* z, const float* f0, const floa
     RVC_HIP(hipMemcpyAsync(d_f0, f0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_g, g, sizeof(float) * B * s.gin, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
-    s.decode(d_z, (long long)s.H * P, d_g, d_f0, d_ns, (int)B, (int)P, d_w);
+    s.decode(d_z, (long long)s.H * P, d_g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P, d_w);
     s.close_span();
     RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
+    RVC_HIP(hipStreamSynchronize(st));
+    s.collect_timing();
+  });
+}
+
+int32_t rvc_synth_decode_chunks(int64_t sh, int64_t n, const float* const* z, const float* const* f0,
+                                const float* const* ns, const float* const* off, const int64_t* P, const float* g,
+                                float* const* wave) {
+  return sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    RVC_CHECK(n >= 1 && n <= 4096, "decode_chunks: chunk count must be in [1, 4096]");
+    RVC_CHECK(z && f0 && ns && P && wave, "decode_chunks: null pointer");
+    for (long long i = 0; i < n; ++i) {
+      RVC_CHECK(z[i] && f0[i] && ns[i] && wave[i], "decode_chunks: null pointer in chunk " + std::to_string(i));
+      s.check_BP(1, P[i]);
+    }
+    // Chunks of one length, with or without phase offsets, run as one batch;
+    // the batches follow each other on the stream with no synchronisation in
+    // between.  Batch rows keep the chunks' order, and a batch's kernels
+    // and tiles depend on (P, rows) only, so every chunk's result equals
+    // its own single-chunk decode.
+    struct Group {
+      long long P;
+      bool off;
+      std::vector<long long> idx;
+    };
+    std::vector<Group> groups;
+    for (long long i = 0; i < n; ++i) {
+      const bool has_off = off && off[i];
+      auto it = std::find_if(groups.begin(), groups.end(),
+                             [&](const Group& gr) { return gr.P == P[i] && gr.off == has_off; });
+      if (it == groups.end()) {
+        groups.push_back(Group{P[i], has_off, {}});
+        it = groups.end() - 1;
+      }
+      it->idx.push_back(i);
+    }
+    // largest batch first, so the workspace is sized once
+    std::stable_sort(groups.begin(), groups.end(), [](const Group& x, const Group& y) {
+      return x.P * (long long)x.idx.size() > y.P * (long long)y.idx.size();
+    });
+    size_t maxBP = 0;
+    for (const Group& gr : groups) maxBP = std::max(maxBP, (size_t)(gr.P * (long long)gr.idx.size()));
+    hipStream_t st = s.eng->stream;
+    float* d_z = s.buf("in_z", maxBP * s.H);
+    float* d_f0 = s.buf("in_f0", maxBP);
+    float* d_off = s.buf("in_off", maxBP);
+    float* d_ns = s.buf("in_ns", maxBP * s.upp);
+    float* d_w = s.buf("out_wave", maxBP * s.upp);
+    float* d_g = nullptr;
+    if (g) {
+      d_g = s.buf("in_g", (size_t)s.gin);
+      RVC_HIP(hipMemcpyAsync(d_g, g, sizeof(float) * s.gin, hipMemcpyHostToDevice, st));
+    }
+    for (const Group& gr : groups) {
+      const long long Pg = gr.P, N = Pg * s.upp;
+      const int Bg = (int)gr.idx.size();
+      for (int r = 0; r < Bg; ++r) {
+        const long long i = gr.idx[r];
+        RVC_HIP(hipMemcpyAsync(d_z + r * s.H * Pg, z[i], sizeof(float) * s.H * Pg, hipMemcpyHostToDevice, st));
+        RVC_HIP(hipMemcpyAsync(d_f0 + r * Pg, f0[i], sizeof(float) * Pg, hipMemcpyHostToDevice, st));
+        RVC_HIP(hipMemcpyAsync(d_ns + r * N, ns[i], sizeof(float) * N, hipMemcpyHostToDevice, st));
+        if (gr.off) RVC_HIP(hipMemcpyAsync(d_off + r * Pg, off[i], sizeof(float) * Pg, hipMemcpyHostToDevice, st));
+      }
+      s.decode(d_z, (long long)s.H * Pg, d_g, 0, d_f0, d_ns, gr.off ? d_off : nullptr, Bg, (int)Pg, d_w);
+      for (int r = 0; r < Bg; ++r)
+        RVC_HIP(hipMemcpyAsync(wave[gr.idx[r]], d_w + r * N, sizeof(float) * N, hipMemcpyDeviceToHost, st));
+    }
+    s.close_span();
     RVC_HIP(hipStreamSynchronize(st));
     s.collect_timing();
   });

@@ -113,6 +113,10 @@ SYMBOLS = {
     "rvc_synth_infer_dev": (I32, [I64] * 10),
     "rvc_synth_decode": (I32, [I64, F32P, F32P, F32P, F32P, I64, I64, F32P]),
     "rvc_synth_decode_dev": (I32, [I64] * 8),
+    "rvc_synth_prep": (I32, [I64, F32P, I64P, F32P, I64P, F32P, I64, I64, I64, F32P, F32P, F32P]),
+    "rvc_synth_phase_offsets": (I32, [I64, F32P, I64, I64, F32P]),
+    "rvc_synth_decode_chunks": (I32, [I64, I64, ctypes.POINTER(F32P), ctypes.POINTER(F32P), ctypes.POINTER(F32P),
+                                      ctypes.POINTER(F32P), I64P, F32P, ctypes.POINTER(F32P)]),
     "rvc_synth_read": (I32, [I64, CHARP, F32P, I64]),
     "rvc_synth_set_precision": (I32, [I64, I32]),
     "rvc_synth_set_debug": (I32, [I64, I32]),

@@ -7,8 +7,9 @@ Tolerance: per-stage relative L2 <= 1e-4 (the engine self-test's op measure,
 engine/test_ffi.py:103-105); the final hidden states are LayerNorm outputs of
 order one, compared at rel L2 <= 1e-4 and max-abs <= 1e-3.  At BASELINE
 config 3's full size (160 000 samples) the oracle comparison runs on a 2 s
-prefix-length input instead, and the full size is checked through shape,
-determinism and batch == per-chunk identity."""
+config 3's full size (160 000 samples, where the attention runs key-split)
+is compared with the oracle too, and checked through shape, determinism and
+batch == per-chunk identity at 2 x 160 000 samples."""
 
 from __future__ import annotations
 
@@ -77,6 +78,25 @@ def test_two_seconds_vs_oracle(sd, hub):
     assert got.shape == want.shape == (1, 99, 768)
     assert rel_l2(got, want) < TOL
     assert np.abs(got - want).max() < 1e-3
+
+
+def test_config3_full_size_vs_oracle(sd, hub):
+    """BASELINE config 3 at full size: 160 000 samples -> [1, 499, 768]."""
+    x = syn.make_hubert_input(160000, seed=5)
+    got = hub.encode(x, version=2)
+    want = H.HubertRef(sd).encode(x, version=2)
+    assert got.shape == want.shape == (1, 499, 768)
+    assert rel_l2(got, want) < TOL
+    assert np.abs(got - want).max() < 1e-3
+
+
+def test_full_size_batch_equals_per_chunk(hub):
+    """Two 10 s chunks (499 frames: key-split attention) as a batch of 2
+    equal the chunks encoded one by one, bit for bit."""
+    xs = [syn.make_hubert_input(160000, seed=s) for s in (11, 12)]
+    both = hub.encode(np.concatenate(xs, axis=0), version=2)
+    for i, x in enumerate(xs):
+        np.testing.assert_array_equal(both[i:i + 1], hub.encode(x, version=2))
 
 
 def test_config3_full_size_properties(hub):

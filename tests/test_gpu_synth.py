@@ -3,10 +3,14 @@
 
 Against the reference's own outputs (golden vectors) and the numpy oracle on
 identical seeded inputs and random-init weights: waveform max-abs <= 1e-3,
-intermediates rel L2 <= 1e-4 (BASELINE.json north_star tolerances).  At the
-full 10 s size the oracle would take minutes, so there the checks are the
-size-independent properties: determinism, batch == per-chunk, finiteness,
-|wave| <= 1, and the first second matching a 1 s oracle run."""
+intermediates rel L2 <= 1e-4 (BASELINE.json north_star tolerances).  The
+BASELINE shapes are checked against the oracle at full size -- config 2
+(P = 1000: enc_p output, flow output and waveform; the attention's key-split
+path), config 4 (48k, 8 chunks of P = 600 as one batch) -- with the oracle's
+"taps" conv formulation (the same mathematics as the reference's einsum form
+in another summation order, pinned against it on the CPU), plus the
+size-independent properties: determinism, batch == per-chunk bit identity,
+finiteness and |wave| <= 1."""
 
 from __future__ import annotations
 
@@ -145,7 +149,7 @@ def test_batch_equals_per_chunk_and_determinism():
     s = _hip_synth(w, sr=geom.sr)
     P = 30
     ins = [syn.make_dec_inputs(geom, P, seed=50 + i) for i in range(3)]
-    outs = s.decode_batch([i["z"] for i in ins], ins[0]["g"], [i["f0"] for i in ins], [i["ns"] for i in ins])
+    outs = s.dec.decode_batch([i["z"] for i in ins], ins[0]["g"], [i["f0"] for i in ins], [i["ns"] for i in ins])
     for i, o in zip(ins, outs):
         one = s.dec_forward(i["z"], i["f0"], ins[0]["g"], i["ns"])
         np.testing.assert_array_equal(o, one)
@@ -190,3 +194,74 @@ def test_end_to_end_1s_vs_oracle():
                                                         inp["nz"], inp["ns"])
     assert np.abs(wave - want).max() <= WAVE_TOL
     assert math.isfinite(float(wave.sum()))
+
+
+def _oracle_enc_out(ref, geom, phone, pitch):
+    """enc_p output [1,H,P] of the oracle (runtime/models/vits.py:2566-2578)."""
+    x = ref.enc_p.embed(phone, pitch) * math.sqrt(geom.hidden)
+    x = nn.leaky_relu(x, 0.1)
+    P = phone.shape[1]
+    return ref.enc_p.encode(x, np.ones((1, 1, P), np.float32)).transpose(0, 2, 1)
+
+
+def test_config2_full_size_vs_oracle():
+    """BASELINE config 2 (40k, P = 1000, B = 1) against the oracle: the
+    encoder output (its attention runs key-split at this length), the flow
+    output and the 400 000-sample waveform."""
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=0)
+    s = _hip_synth(w, sr=geom.sr)
+    ref = V.Synthesizer(w, sr=geom.sr)
+    P, H = 1000, geom.hidden
+    inp = syn.make_synth_inputs(geom, P, seed=3)
+    wave = s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
+    enc_out = s.read("enc_out", (1, H, P))
+    z = s.read("z", (1, H, P))
+    assert rel_l2(enc_out, _oracle_enc_out(ref, geom, inp["phone"], inp["pitch"])) < OP_TOL
+    with nn.conv_formulation("taps"):
+        zr, g = ref.enc_flow(inp["phone"], inp["pitch"], inp["sid"], inp["nz"])
+        assert rel_l2(z, zr) < OP_TOL
+        want = ref.dec.forward(zr, inp["nsff0"], g, inp["ns"])
+    assert wave.shape == want.shape == (1, 1, 400000)
+    assert np.abs(wave - want).max() <= WAVE_TOL
+
+
+def test_config4_48k_batch8_P600():
+    """48k GeneratorNSF, 8 chunks of P = 600 as one batch.
+    Every chunk equals its own single-chunk decode bit for bit; the batch is
+    finite and in tanh range; chunk 5 against the oracle."""
+    geom = syn.GEOM_48K
+    w = syn.make_weights(geom, seed=6)
+    s = _hip_synth(w, sr=geom.sr)
+    P, B = 600, 8
+    ins = [syn.make_dec_inputs(geom, P, seed=400 + i) for i in range(B)]
+    z = np.concatenate([i["z"] for i in ins])
+    f0 = np.concatenate([i["f0"] for i in ins])
+    g = np.concatenate([i["g"] for i in ins])
+    ns = np.concatenate([i["ns"].reshape(1, -1) for i in ins])
+    batch = s.dec_forward(z, f0, g, ns)
+    assert batch.shape == (B, 1, P * geom.upp) == (8, 1, 288000)
+    assert np.isfinite(batch).all() and np.abs(batch).max() <= 1.0
+    for i in range(B):
+        one = s.dec_forward(ins[i]["z"], ins[i]["f0"], ins[i]["g"], ins[i]["ns"])
+        np.testing.assert_array_equal(batch[i:i + 1], one)
+    gen = V.GeneratorNSF(w, V.VitsConfig(w, sr=geom.sr))
+    with nn.conv_formulation("taps"):
+        want = gen.forward(ins[5]["z"], ins[5]["f0"], ins[5]["g"], ins[5]["ns"])
+    assert np.abs(batch[5:6] - want).max() <= WAVE_TOL
+
+
+def test_infer_batch_equals_per_chunk_at_key_split_lengths():
+    """Two P = 256 chunks (attention key-split > 1 at this length) as a batch
+    of 2 equal the same chunks run one by one, bit for bit: the split count
+    and every tile depend on the chunk shape only, never on B."""
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=1)
+    s = _hip_synth(w, sr=geom.sr)
+    P = 256
+    ins = [syn.make_synth_inputs(geom, P, seed=70 + i) for i in range(2)]
+    cat = {k: np.concatenate([i[k] for i in ins]) for k in ("phone", "pitch", "nsff0", "sid", "nz", "ns")}
+    both = s.infer_controlled(cat["phone"], cat["pitch"], cat["nsff0"], cat["sid"], cat["nz"], cat["ns"])
+    for i, inp in enumerate(ins):
+        one = s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
+        np.testing.assert_array_equal(both[i:i + 1], one)

@@ -20,6 +20,7 @@ def _r(*shape):
     return RNG.standard_normal(shape).astype(np.float32)
 
 
+@pytest.mark.parametrize("mode", ["einsum", "taps"])
 @pytest.mark.parametrize("B,C,O,T,K,s,pl,pr,d", [
     (1, 3, 4, 17, 3, 1, 1, 1, 1),
     (2, 2, 3, 20, 5, 1, 4, 4, 2),
@@ -28,9 +29,10 @@ def _r(*shape):
     (1, 2, 2, 9, 3, 2, 0, 1, 1),    # asymmetric padding
     (1, 2, 2, 3, 5, 1, 0, 0, 1),    # kernel longer than input -> empty
 ])
-def test_conv1d_matches_loops(B, C, O, T, K, s, pl, pr, d):
+def test_conv1d_matches_loops(B, C, O, T, K, s, pl, pr, d, mode):
     x, w, b = _r(B, C, T), _r(O, C, K), _r(O)
-    got = nn.conv1d(x, w, b, stride=s, padding=(pl, pr), dilation=d)
+    with nn.conv_formulation(mode):
+        got = nn.conv1d(x, w, b, stride=s, padding=(pl, pr), dilation=d)
     want = loops.conv1d(x, w, b, s, pl, pr, d)
     assert got.shape == want.shape
     if want.size:
@@ -45,15 +47,17 @@ def test_conv1d_matches_scipy_correlate():
     assert rel_l2(got[0], want) < 1e-6
 
 
+@pytest.mark.parametrize("mode", ["einsum", "taps"])
 @pytest.mark.parametrize("C,O,T,K,s,p,op,d", [
     (3, 2, 6, 16, 10, 3, 0, 1),   # dec.ups 0/1 geometry
     (4, 2, 9, 4, 2, 1, 0, 1),     # dec.ups 2/3 geometry
     (2, 3, 5, 24, 12, 6, 0, 1),   # 48k ups 0
     (2, 2, 7, 3, 2, 0, 1, 2),     # output_padding + dilation
 ])
-def test_conv_transpose1d_matches_loops(C, O, T, K, s, p, op, d):
-    x, w, b = _r(1, C, T), _r(C, O, K), _r(O)
-    got = nn.conv_transpose1d(x, w, b, stride=s, padding=p, output_padding=op, dilation=d)
+def test_conv_transpose1d_matches_loops(C, O, T, K, s, p, op, d, mode):
+    x, w, b = _r(2, C, T), _r(C, O, K), _r(O)
+    with nn.conv_formulation(mode):
+        got = nn.conv_transpose1d(x, w, b, stride=s, padding=p, output_padding=op, dilation=d)
     want = loops.conv_transpose1d(x, w, b, s, p, op, d)
     assert got.shape == want.shape
     assert rel_l2(got, want) < 1e-6
@@ -69,6 +73,25 @@ def test_conv_transpose1d_is_adjoint_of_strided_conv():
     lhs = float((yt.astype(np.float64) * y).sum())
     rhs = float((x.astype(np.float64) * cy).sum())
     assert abs(lhs - rhs) < 1e-4 * max(1.0, abs(lhs))
+
+
+def test_conv_formulations_agree_on_a_decoder_stage():
+    """The "taps" formulation used by the full-size parity tests against the
+    reference's einsum formulation on one 40k ResBlock group and one upsample
+    shape (C = 32, k = 11, d = 5; ConvTranspose k16 s10)."""
+    x, w = _r(2, 32, 3000), _r(32, 32, 11)
+    a = nn.conv1d(x, w, None, padding=25, dilation=5)
+    with nn.conv_formulation("taps"):
+        b = nn.conv1d(x, w, None, padding=25, dilation=5)
+    assert rel_l2(b, a) < 1e-6
+    x, w = _r(2, 16, 300), _r(16, 8, 16)
+    a = nn.conv_transpose1d(x, w, None, stride=10, padding=3)
+    with nn.conv_formulation("taps"):
+        b = nn.conv_transpose1d(x, w, None, stride=10, padding=3)
+    assert rel_l2(b, a) < 1e-6
+    with pytest.raises(ValueError):
+        with nn.conv_formulation("fft"):
+            pass
 
 
 def test_layer_norm_softmax_match_loops():
