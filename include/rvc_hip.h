@@ -85,6 +85,15 @@ int32_t rvc_conv1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
 int32_t rvc_conv_t1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
                      int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t padding,
                      int64_t output_padding, int64_t dil);
+/* No reference counterpart: rvc_conv1d for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels
+ * and results as rvc_conv1d; the weights are packed into a fixed 4 MiB device array per GPU instead of
+ * engine scratch, so packed_ld(C_out) * C_in * K (packed_ld = C_out rounded up to 4) must not exceed
+ * 1048576 floats, or the call fails with a message.  The call allocates nothing.  Calls on one GPU
+ * share the array: calls that overlap on one GPU (several engines' streams at once) race. */
+int32_t rvc_conv1d_noalloc(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                           int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t pad_l, int64_t pad_r,
+                           int64_t dil);
 /* No reference counterpart: rvc_conv1d / rvc_conv_t1d computed on bf16 matrix cores with fp32
  * accumulate (inputs and weights rounded to bf16, nearest even; products summed in fp32), for callers
  * that accept bf16 rounding (the config-5 mixed-precision path).  conv1d: stride 1, K <= 11 and

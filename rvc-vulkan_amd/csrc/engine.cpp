@@ -54,6 +54,7 @@ Engine::Engine() {
   const std::string nm = prop.name[0] ? std::string(prop.name) : std::string("AMD GPU");
   device_name = nm + " (" + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) + " CUs)";
   RVC_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  noalloc_setup(device);
   const char* ts = std::getenv("RVC_TS");
   ts_on = ts && std::strcmp(ts, "1") == 0;
 }
@@ -183,9 +184,12 @@ ConvLaunch one_conv(const float* x, long long C_in, long long L, const float* pa
 // Output columns [lo_off, lo_off + n_seg) of the conv1d
 //   out[b][co][o] = bias[co] + sum_{ci,k} w[co][ci][k] x[b][ci][o*stride - pad_l + k*dil]
 // (zero outside [0, L)), written into rows of length row_len.
+// fixed_packed (nullable): where the fp32 MFMA path packs the weights,
+// holding fixed_floats floats, instead of the engine's growable scratch.
 void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
                  long long C_in, long long L, long long C_out, long long K, long long stride, long long pad_l,
-                 long long dil, long long n_seg, long long lo_off, long long row_len, bool bf16 = false) {
+                 long long dil, long long n_seg, long long lo_off, long long row_len, bool bf16 = false,
+                 float* fixed_packed = nullptr, size_t fixed_floats = 0) {
   RVC_CHECK(n_seg >= 1 && lo_off >= 0 && lo_off + n_seg <= row_len, "conv1d: output segment outside the output row");
   check_i32(L, "conv1d"); check_i32(row_len, "conv1d"); check_i32(lo_off * stride + pad_l, "conv1d");
   check_i32(C_in * K, "conv1d"); check_i32(C_out, "conv1d");
@@ -197,6 +201,12 @@ void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, lon
     RVC_CHECK(stride == 1 && conv1d_bf16_supported((int)K, (int)dil),
               "conv1d_bf16: stride 1, K <= " + std::to_string(kConvTapsMax) + " and (K-1)*dil <= " +
                   std::to_string(kConvHaloMax) + " only");
+  const bool mfma = !bf16 && (stride == 1 || stride == 2) && conv1d_mfma_supported((int)K, (int)dil);
+  const size_t packed_floats = (size_t)packed_ld((int)C_out) * C_in * K;
+  if (fixed_packed && mfma)
+    RVC_CHECK(packed_floats <= fixed_floats,
+              "conv1d_noalloc: the packed weights need " + std::to_string(packed_floats) +
+                  " floats (packed_ld(C_out) * C_in * K); the fixed scratch holds " + std::to_string(fixed_floats));
   if (dry) return;
   const long long in_off = lo_off * stride - pad_l;
   if (bf16) {
@@ -210,8 +220,8 @@ void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, lon
     a.ob = C_out * row_len;
     a.oc = row_len;
     launch_conv1d_bf16(a, e.stream);
-  } else if ((stride == 1 || stride == 2) && conv1d_mfma_supported((int)K, (int)dil)) {
-    float* packed = static_cast<float*>(e.scratch_for(sizeof(float) * packed_ld((int)C_out) * C_in * K));
+  } else if (mfma) {
+    float* packed = fixed_packed ? fixed_packed : static_cast<float*>(e.scratch_for(sizeof(float) * packed_floats));
     launch_pack_conv_weight(wp, packed, (int)C_out, (int)C_in, (int)K, e.stream);
     ConvLaunch a = one_conv(xp, C_in, L, packed, bp, op, C_out, n_seg, B, K, dil, pad_l, stride);
     a.g[0].in_off = (int)in_off;
@@ -233,13 +243,15 @@ void conv1d_core(Engine& e, bool dry, long long x, long long w, long long b, lon
 
 void op_conv1d(Engine& e, bool dry, long long x, long long w, long long b, long long out, long long B,
                long long C_in, long long L, long long C_out, long long K, long long stride, long long pad_l,
-               long long pad_r, long long dil, bool bf16 = false) {
+               long long pad_r, long long dil, bool bf16 = false, float* fixed_packed = nullptr,
+               size_t fixed_floats = 0) {
   RVC_CHECK(B >= 1 && C_in >= 1 && C_out >= 1 && K >= 1 && stride >= 1 && dil >= 1 && pad_l >= 0 &&
                 pad_r >= 0 && L >= 0,
             "conv1d: invalid parameters (stride/dilation>=1, padding>=0, K>=1)");
   const long long n_out = (L + pad_l + pad_r - dil * (K - 1) - 1) / stride + 1;
   RVC_CHECK(L + pad_l + pad_r - dil * (K - 1) - 1 >= 0 && n_out >= 1, "conv1d: empty output");
-  conv1d_core(e, dry, x, w, b, out, B, C_in, L, C_out, K, stride, pad_l, dil, n_out, 0, n_out, bf16);
+  conv1d_core(e, dry, x, w, b, out, B, C_in, L, C_out, K, stride, pad_l, dil, n_out, 0, n_out, bf16, fixed_packed,
+              fixed_floats);
 }
 
 // engine/src/ffi.zig:703-751: the output segment [lo_off, lo_off + seg_len)
@@ -993,6 +1005,20 @@ int32_t rvc_conv1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int6
 int32_t rvc_conv_t1d(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t l,
                      int64_t c_out, int64_t k, int64_t stride, int64_t padding, int64_t output_padding, int64_t dil) {
   return single(h, 5, x, w, b, {B, c_in, l, c_out, k, stride, padding, output_padding, dil, out});
+}
+
+int32_t rvc_conv1d_noalloc(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in,
+                           int64_t l, int64_t c_out, int64_t k, int64_t stride, int64_t pad_l, int64_t pad_r,
+                           int64_t dil) {
+  // rvc_conv1d's kernels with the packed weights in the device's fixed
+  // scratch: no hipMalloc / hipFree, no event, no library allocation
+  return guarded(h, [&](Engine& e) {
+    float* fixed = noalloc_scratch(e.device);
+    op_conv1d(e, true, x, w, b, out, B, c_in, l, c_out, k, stride, pad_l, pad_r, dil, false, fixed,
+              kNoAllocScratchFloats);
+    op_conv1d(e, false, x, w, b, out, B, c_in, l, c_out, k, stride, pad_l, pad_r, dil, false, fixed,
+              kNoAllocScratchFloats);
+  });
 }
 
 int32_t rvc_conv1d_bf16(int64_t h, int64_t x, int64_t w, int64_t b, int64_t out, int64_t B, int64_t c_in, int64_t l,

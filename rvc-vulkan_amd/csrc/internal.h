@@ -225,6 +225,14 @@ inline int convt_phase_taps(int K, int st, int r) { return r < K ? (K - r + st -
 // Weight packing kernels (device side, used by the op-level ABI).
 // [C_out][C_in][K] -> [K][C_in][packed_ld(C_out)] (pad columns zero)
 void launch_pack_conv_weight(const float* w, float* out, int C_out, int C_in, int K, hipStream_t s);
+
+// ---------------------------------------------------------------- fixed scratch (noalloc.hip)
+// Per-GPU static device array behind the entry points that allocate nothing:
+// 1 Mi floats (4 MiB).  noalloc_setup(device) looks up the array's address on
+// `device` (which must be current) once; noalloc_scratch returns it.
+constexpr size_t kNoAllocScratchFloats = (size_t)1 << 20;
+void noalloc_setup(int device);
+float* noalloc_scratch(int device);
 // ConvTranspose [C_in][C_out][K], phase r of stride st with J taps:
 // out[j'][ci][co] = w[ci][co][r + (J-1-j')*st], ld packed_ld(C_out)
 void launch_pack_convt_phase(const float* w, float* out, int C_in, int C_out, int K, int st, int r,

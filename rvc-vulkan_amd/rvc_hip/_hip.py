@@ -58,6 +58,7 @@ SYMBOLS = {
     "rvc_mem_upload_to_batch": (I32, [I64, I64, I64P, ctypes.POINTER(F32P), I64P]),
     "rvc_mem_download_batch": (I32, [I64, I64P, ctypes.POINTER(ctypes.POINTER(ctypes.c_uint8)), I64P, I64]),
     "rvc_matmul": (I32, [I64] * 7),
+    "rvc_conv1d_noalloc": (I32, [I64] * 14),
     "rvc_add": (I32, [I64] * 5),
     "rvc_mul": (I32, [I64] * 5),
     "rvc_relu": (I32, [I64] * 3),
