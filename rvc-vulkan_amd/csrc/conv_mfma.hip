@@ -208,7 +208,9 @@ void conv1d_mfma_kernel(ConvLaunch a) {
     const int c4 = idx - row * W4ROW;
     const int k = row / BKT;
     const int rr = row - k * BKT;
-    const bool ok = idx < nw4 && co0 + 4 * c4 < a.w_ld;
+    // columns past C_out (rounded up to 4) are never stored: not loaded either, so a
+    // group whose weights start inside a wider packed row stays inside it
+    const bool ok = idx < nw4 && co0 + 4 * c4 < ((a.C_out + 3) & ~3);
     wr_[e] = ok ? rr : 1 << 30;
     wo[e] = ok ? (k * a.C_in + rr) * a.w_ld + co0 + 4 * c4 : 0;
   }
@@ -502,7 +504,8 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
       const int c4 = idx - row * W4ROW;
       const int k = row / BKT;
       const int rr = row - k * BKT;
-      wo[e] = idx < nw4 && s_co0 + 4 * c4 < a.w_ld ? 4u * (unsigned)((k * a.C_in + rr) * a.w_ld + s_co0 + 4 * c4)
+      wo[e] = idx < nw4 && s_co0 + 4 * c4 < ((a.C_out + 3) & ~3)
+                  ? 4u * (unsigned)((k * a.C_in + rr) * a.w_ld + s_co0 + 4 * c4)
                                                     : kOut;
     }
   };

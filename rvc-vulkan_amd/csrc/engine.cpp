@@ -677,7 +677,11 @@ void op_gru(Engine& e, bool dry, long long a_, long long b_, long long c_, long 
   }
   g.state = e.gru_state;
   g.sync = reinterpret_cast<unsigned*>(e.gru_state + 2 * 2 * 256);
-  launch_bigru(g, e.stream);  // its init kernel clears the flag first
+  // the error flag is sticky until check_gru reads it: the first GRU since
+  // the last check clears it, later ones of the same batch keep a timeout
+  // an earlier one reported
+  g.keep_err = e.gru_pending ? 1 : 0;
+  launch_bigru(g, e.stream);
   e.gru_pending = true;
 }
 

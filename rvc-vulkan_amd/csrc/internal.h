@@ -403,6 +403,7 @@ struct GruArgs {
   unsigned* sync;                               // [4]: arrivals per direction, error flag
   int T, H;
   long long spin_limit;
+  int keep_err;  // 1: leave the error flag as an earlier, unchecked GRU left it
 };
 void launch_bigru(const GruArgs& g, hipStream_t s);
 void launch_rmvpe_decode(const float* sal, long long s_f, long long s_k, int F, int nb, const float* cents,

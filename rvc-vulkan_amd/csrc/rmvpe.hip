@@ -583,10 +583,11 @@ __device__ __forceinline__ unsigned long long gru_word(int tag, float v) {
   return ((unsigned long long)(unsigned)tag << 32) | (unsigned long long)__float_as_uint(v);
 }
 
-__global__ void gru_init_kernel(unsigned long long* state, unsigned* sync) {
+__global__ void gru_init_kernel(unsigned long long* state, unsigned* sync, int keep_err) {
   // buffer 1 holds h_{-1} = 0 tagged -1; buffer 0 a tag no step waits for
   for (int k = threadIdx.x; k < 2 * 2 * 256; k += blockDim.x) state[k] = gru_word(((k >> 8) & 1) ? -1 : -2, 0.f);
-  if (threadIdx.x < 4) sync[threadIdx.x] = 0u;
+  // sync[2] is the error flag: kept when an earlier GRU's flag still awaits its check
+  if (threadIdx.x < 4 && !(threadIdx.x == 2 && keep_err)) sync[threadIdx.x] = 0u;
 }
 
 __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
@@ -687,7 +688,7 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
 void launch_bigru(const GruArgs& g, hipStream_t s) {
   RVC_CHECK(g.T >= 1 && g.H >= 1 && g.H <= kGruGroups * kGruUnits, "bigru: need T >= 1 and 1 <= H <= 256");
   RVC_CHECK(g.state && g.sync && g.gx && g.whh && g.bhh && g.out && g.spin_limit > 0, "bigru: null argument");
-  hipLaunchKernelGGL(gru_init_kernel, dim3(1), dim3(256), 0, s, g.state, g.sync);
+  hipLaunchKernelGGL(gru_init_kernel, dim3(1), dim3(256), 0, s, g.state, g.sync, g.keep_err);
   check_launch("gru_init");
   hipLaunchKernelGGL(bigru_kernel, dim3(2 * kGruGroups), dim3(256), 0, s, g);
   check_launch("bigru");

@@ -1,9 +1,15 @@
 # -*- coding: utf-8 -*-
 """Write tests/golden/reference_loader_symbols.json: every symbol the
 reference's ctypes loader binds (runtime/_vulkan.py:148-278) with its
-argument count and return type, so the CPU tests can check that
+return type and the type of each argument, so the CPU tests can check that
 librvc_hip.so is loadable through that loader (it sets restype/argtypes on
-all of them with no try/except).
+all of them with no try/except) and that every argument has the C type the
+loader passes (an int64 / pointer / double mix-up would otherwise pass
+silently).
+
+Argument types are written as canonical tokens: I32, I64, F32P (float*),
+I64P (int64*), F32PP (float**), U8PP (uint8**), VOIDP (void*), CHARP
+(char*) and DOUBLE.
 
 The loader is read as text and parsed (not imported or evaluated): the
 argtypes expressions there are list literals, ``[T] * N`` and
@@ -40,10 +46,18 @@ def _split_top(s: str) -> list:
     return parts
 
 
-def _count(expr: str) -> int:
-    """Number of entries of an argtypes expression: a sum of terms, each a
-    list literal optionally repeated (``* N``)."""
-    total = 0
+_TOKENS = {
+    "I32": "I32", "I64": "I64", "F32_PTR": "F32P", "CHAR_PTR": "CHARP",
+    "ctypes.POINTER(I64)": "I64P", "ctypes.POINTER(F32_PTR)": "F32PP",
+    "ctypes.POINTER(ctypes.POINTER(ctypes.c_uint8))": "U8PP",
+    "ctypes.c_void_p": "VOIDP", "ctypes.c_double": "DOUBLE",
+}
+
+
+def _types(expr: str) -> list:
+    """Argument type tokens of an argtypes expression: a sum of terms, each
+    a list literal optionally repeated (``* N``)."""
+    out = []
     for term in re.split(r"\]\s*\+\s*\[", expr):
         term = term.strip()
         term = term if term.startswith("[") else "[" + term
@@ -51,8 +65,11 @@ def _count(expr: str) -> int:
         if not m:
             raise ValueError(f"unparsed argtypes term: {term!r}")
         body, rep = m.group(1), int(m.group(2) or 1)
-        total += len(_split_top(body)) * rep
-    return total
+        toks = [_TOKENS[" ".join(e.split()).replace(" ", "")] if e else None for e in _split_top(body)]
+        if None in toks:
+            raise ValueError(f"empty argtypes entry in {term!r}")
+        out += toks * rep
+    return out
 
 
 def main() -> int:
@@ -61,9 +78,9 @@ def main() -> int:
     res = dict(re.findall(r"dll\.(rvc_\w+)\.restype\s*=\s*(\w+)", text))
     args = {}
     for m in re.finditer(r"dll\.(rvc_\w+)\.argtypes\s*=\s*(\[.*?\](?:\s*\+\s*\[.*?\])*(?:\s*\*\s*\d+)?)", text, re.S):
-        args[m.group(1)] = _count(" ".join(m.group(2).split()))
+        args[m.group(1)] = _types(" ".join(m.group(2).split()))
     assert set(res) == set(args), sorted(set(res) ^ set(args))
-    rows = {k: {"nargs": args[k], "restype": res[k]} for k in sorted(res)}
+    rows = {k: {"nargs": len(args[k]), "args": args[k], "restype": res[k]} for k in sorted(res)}
     with open(OUT, "w") as f:
         json.dump({"source": "runtime/_vulkan.py:148-278", "symbols": rows}, f, indent=1, sort_keys=True)
     print(f"{len(rows)} symbols -> {OUT}")

@@ -100,20 +100,64 @@ def test_synthetic_generator_is_seeded():
     assert (f0 == 0).mean() >= 0.2 and f0.max() <= 400 and f0[f0 > 0].min() >= 80
 
 
+def _ctypes_token(t):
+    """Canonical token of a ctypes argument type (see make_loader_symbols.py)."""
+    P = ctypes.POINTER
+    table = {ctypes.c_int32: "I32", ctypes.c_int64: "I64", P(ctypes.c_float): "F32P", P(ctypes.c_int64): "I64P",
+             P(P(ctypes.c_float)): "F32PP", P(P(ctypes.c_uint8)): "U8PP", ctypes.c_void_p: "VOIDP",
+             ctypes.c_char_p: "CHARP", P(ctypes.c_char): "CHARP", ctypes.c_double: "DOUBLE",
+             P(ctypes.c_double): "F64P", P(ctypes.c_int16): "I16P"}
+    return table[t]
+
+
+def _header_decls():
+    """name -> argument type tokens of every prototype in include/rvc_hip.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    c_tok = {"int64_t": "I64", "int32_t": "I32", "float*": "F32P", "int64_t*": "I64P", "float**": "F32PP",
+             "uint8_t**": "U8PP", "void*": "VOIDP", "char*": "CHARP", "double": "DOUBLE", "double*": "F64P",
+             "int16_t*": "I16P"}
+    out = {}
+    for m in re.finditer(r"\b(?:int32_t|int64_t)\s+(rvc_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        toks = []
+        for a in args:
+            # "<base> <*...> <name>", const dropped: e.g. "const float* const* z" -> float**
+            m2 = re.fullmatch(r"(\w+)\s*((?:\*\s*)*)(\w+)?", re.sub(r"\bconst\b", " ", a).strip())
+            assert m2, (m.group(1), a)
+            toks.append(c_tok[m2.group(1) + m2.group(2).replace(" ", "")])
+        out[m.group(1)] = toks
+    return out
+
+
 def test_reference_loader_symbols_bind(hip):
     """Every symbol the reference's ctypes loader binds (runtime/_vulkan.py:
-    148-278, no try/except) is exported with the same argument count and
-    return width, so that loader can load librvc_hip.so via RVC_CORE_DLL."""
+    148-278, no try/except) is exported with the same return width and, one
+    by one, the same argument types -- in this package's ctypes table and in
+    the C prototypes of include/rvc_hip.h the library is compiled against --
+    so that loader can drive librvc_hip.so via RVC_CORE_DLL."""
     with open(os.path.join(GOLDEN, "reference_loader_symbols.json")) as f:
         ref = json.load(f)["symbols"]
     assert len(ref) == 56
     lib = ctypes.CDLL(hip.so_path)
     width = {"I32": ctypes.c_int32, "I64": ctypes.c_int64}
+    decls = _header_decls()
     for name, spec in ref.items():
         assert hasattr(lib, name), name
         res, args = hip.SYMBOLS[name]
-        assert len(args) == spec["nargs"], (name, len(args), spec["nargs"])
+        assert len(args) == spec["nargs"] == len(spec["args"]), (name, len(args), spec["nargs"])
+        assert [_ctypes_token(a) for a in args] == spec["args"], name
+        assert decls[name] == spec["args"], (name, decls[name])
         assert res is width[spec["restype"]], name
+
+
+def test_header_and_ctypes_table_agree(hip):
+    """Every prototype of include/rvc_hip.h has the same argument types in
+    rvc_hip._hip.SYMBOLS, and the two name the same exports."""
+    decls = _header_decls()
+    assert set(decls) == set(hip.SYMBOLS)
+    for name, toks in decls.items():
+        assert [_ctypes_token(a) for a in hip.SYMBOLS[name][1]] == toks, name
 
 
 def test_not_provided_exports_fail_with_message(hip):
