@@ -10,7 +10,10 @@ z_p noise nz and the NSF noise ns), ending with a stream synchronize.
 Prints ONE JSON line with the metric, the roofline of the dominant kernel
 (the fp32 MFMA implicit-GEMM ResBlock convolutions, timed with HIP events on
 the session stream over the timed steps) and a CPU baseline (the numpy
-oracle on a bounded 1 s sample of the same workload, on this host).
+oracle on a bounded 4 s sample of the same workload, on this host).  The
+host-in / host-out rate (numpy arrays in, numpy waveform out, PCIe copies
+included; the median of 20 calls after 3 warm-ups) is reported beside it as
+``host_io_audio_s_per_s``; ``value`` is the device-resident rate.
 
 ``--workload hubert`` measures BASELINE config 3 instead (HuBERT-base
 encoder, 10 s of 16 kHz audio -> [1, 499, 768]), ``--workload dec48k-b8``
@@ -84,19 +87,39 @@ def profiled_traffic():
     return int(m.group(1)) if m else None
 
 
+def host_cpu():
+    """Model name, physical cores and logical threads of this host (from
+    /proc/cpuinfo, which is what lscpu reads)."""
+    model, cores = "unknown", set()
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                k, _, v = ln.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+            if phys is not None:
+                cores.add((phys, core))
+    except OSError:
+        pass
+    return {"model": model, "physical_cores": len(cores) or None, "threads": os.cpu_count()}
+
+
 def cpu_baseline(w, geom):
-    """The numpy oracle (a restatement of the reference numpy path) on a 1 s
+    """The numpy oracle (a restatement of the reference numpy path) on a 4 s
     sample of the same workload; returns audio-seconds per second."""
     from oracle import vits_ref
     from rvc_hip import synthetic as syn
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"),
-                      default=1)
-    except Exception:  # noqa: BLE001
-        threads = 1
+    threads = _blas_threads()
     ref = vits_ref.Synthesizer(w, sr=geom.sr)
     inp = syn.make_synth_inputs(geom, CPU_SAMPLE_FRAMES, seed=7)
     ref.infer_controlled(inp["phone"][:, :10], inp["pitch"][:, :10], inp["nsff0"][:, :10], inp["sid"],
@@ -107,7 +130,8 @@ def cpu_baseline(w, geom):
     audio_s = CPU_SAMPLE_FRAMES / 100.0
     return {"value": audio_s / dt, "unit": "audio-s/s", "cores": int(threads), "kind": "port",
             "sample": f"{CPU_SAMPLE_FRAMES / 100:g} s (P={CPU_SAMPLE_FRAMES}) of the config-2 synthesis (same weights, 40k), "
-                      f"numpy oracle, 1 run after a warm-up, {dt:.2f} s wall"}
+                      f"numpy oracle, 1 run after a warm-up, {dt:.2f} s wall",
+            "host": host_cpu(), "blas_threads": int(threads)}
 
 
 def calibrate_copy(mib: int):
@@ -638,7 +662,8 @@ def main():
     value = audio_s * args.steps / dt
     _log(f"bench: {args.steps} steps, {ms_step:.3f} ms/step, {value:.1f} audio-s/s")
 
-    # roofline of the dominant kernel family (ResBlock MFMA convs, 216 launches/step)
+    # roofline of the dominant kernel family (the ResBlock MFMA convs, one launch per
+    # dilation group and conv of each of the four stages: 24 launches per step)
     n_launch = max(rb["launches"], 1)
     avg_s = rb["ms"] / 1e3 / n_launch
     flops_launch = rb["flops"] / n_launch
@@ -660,13 +685,20 @@ def main():
         breakdown[tag] = family_entry(s.get_timing())
     s.set_timing("")
 
-    # PCIe-inclusive rate (host numpy in -> host numpy out); reported, never the headline
-    host_io = None
+    # PCIe-inclusive rate (host numpy in -> host numpy out): the median of 20
+    # calls after 3 warm-ups; reported beside the device-resident headline
+    host_io = host_io_ms = None
     if not args.quick:
-        t0 = time.perf_counter()
+        call = lambda: s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])  # noqa: E731
         for _ in range(3):
-            s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
-        host_io = round(audio_s * 3 / (time.perf_counter() - t0), 2)
+            call()
+        times = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            call()
+            times.append(time.perf_counter() - t0)
+        host_io_ms = float(np.median(times)) * 1e3
+        host_io = round(audio_s / (host_io_ms / 1e3), 2)
 
     cpu = None if (args.no_cpu_baseline or args.quick) else cpu_baseline(w, geom)
     line = {
@@ -676,7 +708,9 @@ def main():
         "config": {"workload": "config 2: RVC v2 40k enc_p+flow+GeneratorNSF, 10 s (P=1000), batch 1, fp32",
                    "frames": P, "batch": B, "sample_rate": SR, "output_samples": n_out},
         "roofline": roofline, "cpu_baseline": cpu,
-        "host_io_audio_s_per_s": host_io, "breakdown": breakdown,
+        "host_io_audio_s_per_s": host_io,
+        "host_io_ms_median": None if host_io_ms is None else round(host_io_ms, 4),
+        "breakdown": breakdown,
     }
     print(json.dumps(line), flush=True)
 
