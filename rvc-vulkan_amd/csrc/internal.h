@@ -222,6 +222,29 @@ void convt_polyphase_bf16(hipStream_t st, const float* x, long long xb, long lon
 // taps of phase r of a stride-st ConvTranspose with K taps
 inline int convt_phase_taps(int K, int st, int r) { return r < K ? (K - r + st - 1) / st : 0; }
 
+// Output-stationary polyphase ConvTranspose1d + bias + the NSF noise term
+// (convt_os.hip):
+//   out[b][co][o] = (sum_{ci,k} w[k][ci][co] lrelu(x[b][ci][m-j]) + bias[co]) + noise
+//   with o + pad = m*S + r, k = r + j*S; noise = noise[b][co][o] when the
+//   tensor is given, else (sum_{t<kn} nw[co][t] har[b][o*ns - np + t]) + nb[co].
+constexpr int kNoiseTapsMax = 8;  // longest noise kernel computed in the epilogue
+struct ConvTOsLaunch {
+  const float* x; long long xb; int L_in;       // input [B][C_in][L_in]
+  const float* w; int w_ld;                     // packed [K][C_in][w_ld], 16-byte rows
+  const float* bias;                            // [C_out] or null
+  float* out; long long ob, oc; int L_out;      // [B][C_out (stride oc)][L_out]
+  int B, C_in, C_out, K, S, pad;
+  int M;                                        // input positions covered: ceil((L_out + pad) / S)
+  float in_slope;                               // leaky ReLU on the staged input
+  const float* noise;                           // [B][C_out][L_out] (strides ob, oc) or null
+  const float* har; long long harb; long long N;  // harmonic source [B][N]
+  const float* nw; const float* nb; int kn, ns, np;  // noise conv [C_out][kn], [C_out]
+};
+// (K, S) shapes the kernel is instantiated for: (16, 10), (20, 10), (24, 12), (4, 2)
+bool convt_os_supported(int K, int S);
+// false when no instantiation fits (C_out / C_in multiples)
+bool launch_convt_os(const ConvTOsLaunch& a, hipStream_t s);
+
 // Weight packing kernels (device side, used by the op-level ABI).
 // [C_out][C_in][K] -> [K][C_in][packed_ld(C_out)] (pad columns zero)
 void launch_pack_conv_weight(const float* w, float* out, int C_out, int C_in, int K, hipStream_t s);

@@ -68,6 +68,10 @@ struct Synth : SessionBase {
     float* rb[3][2][3];
     std::vector<uint16_t*> phases16;  // precision >= 1
     uint16_t* rw16[3][2][3];          // precision 2, else null
+    // fp32 output-stationary ConvTranspose (convt_os_supported shapes): all
+    // taps packed [K][C_in][packed_ld(C)]; null when the polyphase grids run
+    float* up_all = nullptr;
+    bool noise_fused = false;  // the stage's noise conv is computed by that kernel
   };
   std::vector<StageW> stages;
 
@@ -80,6 +84,7 @@ struct Synth : SessionBase {
   hipStream_t side = nullptr;
   hipEvent_t forked = nullptr, joined = nullptr;
   float* dec_cv = nullptr;
+  float* dec_har = nullptr;  // the harmonic source of the current call (side stream)
   std::vector<float*> dec_noise;
 
   ~Synth() override {
@@ -316,6 +321,14 @@ struct Synth : SessionBase {
       const int kn = (int)nw.shape[2];
       noise_k.push_back(kn);
       noise_s.push_back(i < n_ups - 1 ? kn / 2 : 1);
+      if (!b16 && convt_os_supported(K, st) && c_in % 8 == 0 && c % 32 == 0) {
+        std::vector<float> all((size_t)K * c_in * ld, 0.f);  // [k][ci][co] = wt[ci][co][k]
+        for (int k = 0; k < K; ++k)
+          for (int ci = 0; ci < c_in; ++ci)
+            for (int co = 0; co < c; ++co) all[((size_t)k * c_in + ci) * ld + co] = wt[((size_t)ci * c + co) * K + k];
+        S.up_all = upload(all);
+        S.noise_fused = kn <= kNoiseTapsMax;
+      }
       S.nw = upload_key(nc + ".weight");
       S.nb = upload_vec(nc + ".bias", c);
       static const int ks[3] = {3, 7, 11};
@@ -515,6 +528,7 @@ struct Synth : SessionBase {
     }
     const long long N = (long long)P * upp;
     float* har = buf("har", (size_t)B * N);
+    dec_har = har;
     float* phase = buf("phase", (size_t)B * P);
     dec_cv = buf("dec_cond", (size_t)B * U);
     dec_noise.assign(n_ups, nullptr);
@@ -542,6 +556,7 @@ struct Synth : SessionBase {
       const int C = chans[i];
       L *= rates[i];
       const long long CL = (long long)C * L;
+      if (stages[i].noise_fused) continue;  // formed by the stage's ConvTranspose kernel
       DirectConvArgs d{};
       d.x = har; d.xb = N; d.xc = N;
       d.w = stages[i].nw; d.bias = stages[i].nb;
@@ -593,24 +608,48 @@ struct Synth : SessionBase {
       const int Lo = L * rates[i];
       const long long CL = (long long)C * Lo;
       float* X = dec_noise[i];
-      // ups: X += ConvTranspose1d(lrelu(cur, 0.1)) + bias
+      // ups: X = ConvTranspose1d(lrelu(cur, 0.1)) + bias + noise_conv(har)
       {
         const int K = kernels[i], st = rates[i], pad = (K - st) / 2;
         const int n_out = (L - 1) * st - 2 * pad + K;
         RVC_CHECK(n_out == Lo, "ConvTranspose output length must equal L * rate");
         std::vector<const float*> ph(stages[i].phases.begin(), stages[i].phases.end());
         std::snprintf(tg, sizeof tg, "dec.ups.s%d", i);
-        run(tg, 2.0 * B * (double)c_in * C * K * L, 4.0 * B * ((double)c_in * L + 2.0 * CL) + 4.0 * c_in * C * K,
-            [&] {
-              if (!stages[i].phases16.empty()) {
-                std::vector<const uint16_t*> p16(stages[i].phases16.begin(), stages[i].phases16.end());
-                convt_polyphase_bf16(s, cur, (long long)c_in * L, L, p16.data(), bf16_ld(c_in), stages[i].up_b, X, CL,
-                                     Lo, B, c_in, C, L, Lo, K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
-              } else {
-                convt_polyphase(s, cur, (long long)c_in * L, L, ph.data(), stages[i].up_b, X, CL, Lo, B, c_in, C, L, Lo,
-                                K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
-              }
-            });
+        const StageW& SW = stages[i];
+        if (SW.up_all) {
+          // one output-stationary launch: ConvTranspose + bias + the noise
+          // term (computed from har, or read from the side stream's buffer)
+          ConvTOsLaunch o{};
+          o.x = cur; o.xb = (long long)c_in * L; o.L_in = L;
+          o.w = SW.up_all; o.w_ld = packed_ld(C); o.bias = SW.up_b;
+          o.out = X; o.ob = CL; o.oc = Lo; o.L_out = Lo;
+          o.B = B; o.C_in = c_in; o.C_out = C; o.K = K; o.S = st; o.pad = pad;
+          o.M = (Lo + pad + st - 1) / st;
+          o.in_slope = 0.1f;
+          o.noise = SW.noise_fused ? nullptr : X;
+          o.har = dec_har; o.harb = (long long)P * upp; o.N = (long long)P * upp;
+          o.nw = SW.nw; o.nb = SW.nb; o.kn = noise_k[i]; o.ns = noise_s[i]; o.np = noise_s[i] / 2;
+          const double nflop = SW.noise_fused ? 2.0 * B * CL * noise_k[i] : 0.0;
+          const double nbytes = SW.noise_fused ? 4.0 * B * (double)P * upp : 8.0 * B * CL;
+          run(tg, 2.0 * B * (double)c_in * C * K * L + nflop,
+              4.0 * B * ((double)c_in * L + CL) + nbytes + 4.0 * c_in * C * K, [&] {
+                RVC_CHECK(launch_convt_os(o, s), "dec: no ConvTranspose tile fits stage " + std::to_string(i));
+              });
+        } else {
+          // one grid of `stride` polyphase convolutions accumulating onto the
+          // noise conv's output
+          run(tg, 2.0 * B * (double)c_in * C * K * L, 4.0 * B * ((double)c_in * L + 2.0 * CL) + 4.0 * c_in * C * K,
+              [&] {
+                if (!SW.phases16.empty()) {
+                  std::vector<const uint16_t*> p16(SW.phases16.begin(), SW.phases16.end());
+                  convt_polyphase_bf16(s, cur, (long long)c_in * L, L, p16.data(), bf16_ld(c_in), SW.up_b, X, CL, Lo,
+                                       B, c_in, C, L, Lo, K, st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
+                } else {
+                  convt_polyphase(s, cur, (long long)c_in * L, L, ph.data(), SW.up_b, X, CL, Lo, B, c_in, C, L, Lo, K,
+                                  st, pad, ACT_LEAKY, 0.1f, COMB_ADD);
+                }
+              });
+        }
       }
       // three ResBlock1 (k = 3, 7, 11) run side by side: each conv launch
       // carries the same dilation group of all three blocks (k = 11 first, so
