@@ -52,6 +52,18 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
+// A buffer resource from values the whole wave shares.  readfirstlane keeps
+// the descriptor in scalar registers even where the compiler placed one of
+// its inputs in a vector register (a descriptor in vector registers turns
+// every load through it into a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, unsigned range) {
+  const unsigned long long v = reinterpret_cast<unsigned long long>(base);
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+  void* p = reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)__builtin_amdgcn_readfirstlane(range), 0x00020000);
+}
+
 __device__ __forceinline__ float apply_act(float v, int act, float slope) {
   if (act == ACT_LEAKY) return v >= 0.f ? v : v * slope;
   if (act == ACT_TANH) return tanhf(v);
@@ -517,10 +529,8 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     // the weight rows k * C_in + ci0 + rr of every tap
     const unsigned xr = 4u * (unsigned)((a.C_in - ci0 - 1) * (int)a.xc + a.L_in);
     const unsigned wr = 4u * (unsigned)(((s_K - 1) * a.C_in + a.C_in - ci0) * a.w_ld);
-    const __amdgpu_buffer_rsrc_t xrs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(s_x + (long long)ci0 * a.xc), (short)0, (int)xr, 0x00020000);
-    const __amdgpu_buffer_rsrc_t wrs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(s_w + (long long)ci0 * a.w_ld), (short)0, (int)wr, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(s_x + (long long)ci0 * a.xc, xr);
+    const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(s_w + (long long)ci0 * a.w_ld, wr);
 #pragma unroll
     for (int e = 0; e < XPT; ++e) xv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xo[e], 0, 0));
 #pragma unroll
@@ -624,7 +634,9 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     }
     // the last chunk: prefetch the next item's first chunk and this item's
     // epilogue operand (the residual, or the current output for ADD)
-    const int next = next_sh;
+    // the same value in every lane: readfirstlane tells the compiler so, and
+    // the next item's geometry, pointers and buffer resources stay scalar
+    const int next = __builtin_amdgcn_readfirstlane(next_sh);
     const bool more = next < n_items;
     if (more) {
       setup(next);
@@ -638,12 +650,9 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     const bool res = G.res != nullptr;
     const bool add = G.combine == COMB_ADD;
     const int co_l = c_co0 + wm * WM + 4 * half;
-    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(G.out + (long long)c_b * a.ob), (short)0, (int)(4u * (unsigned)(a.C_out * (int)a.oc)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(G.out + (long long)c_b * a.ob, 4u * (unsigned)(a.C_out * (int)a.oc));
     const __amdgpu_buffer_rsrc_t prs =
-        res ? __builtin_amdgcn_make_buffer_rsrc((void*)(G.res + (long long)c_b * a.rb), (short)0,
-                                                (int)(4u * (unsigned)(a.C_out * (int)a.rc)), 0x00020000)
-            : ors;
+        res ? uniform_rsrc(G.res + (long long)c_b * a.rb, 4u * (unsigned)(a.C_out * (int)a.rc)) : ors;
     const int pc = res ? (int)a.rc : (int)a.oc;
     unsigned ooff[TN], poff[TN];
 #pragma unroll
