@@ -707,6 +707,188 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     for (int i = 0; i < 9; ++i) __hip_atomic_store(a.queue + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
+// Small 1x1 GEMMs (enc_p / flow projections at a few thousand frames): the
+// whole reduction of a 32 x BN output tile -- x[0:C_in][i0:i0+BN] and
+// W[0:C_in][co0:co0+32], C_in <= 256 -- is staged into LDS with one round of
+// loads, the four waves each take a quarter of the input channels for the
+// full tile, and the quarters are added through LDS in wave order
+// (((q0 + q1) + q2) + q3), then + bias (+ bias2) (+ residual), activation
+// and combine, in the split-K reduce's order.  One launch, one load latency
+// and no partial-sum tensor, where the chunked kernel pays a load round trip
+// per channel chunk and a separate reduce.
+template <int BN>
+__global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
+  constexpr int TN = BN / 32;
+  constexpr int RS = 256 / BN;        // input channels one pass of the workgroup stages
+  constexpr int KO = 32 * BN / 256;   // outputs each thread forms
+  constexpr int LB = 16;              // loads in flight per thread per staging batch
+  constexpr unsigned kOut = 0x80000000u;
+  extern __shared__ float smem[];
+  const int b = blockIdx.z % a.B;
+  const int gi = blockIdx.z / a.B;
+  const ConvGroup& G = a.g[gi];
+  const int i0 = blockIdx.x * BN;
+  if (i0 >= G.n_out) return;  // uniform for the whole workgroup, before any barrier
+  const int co0 = blockIdx.y * 32;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int C_in = a.C_in;
+  // LDS: ws [256][32] (rows past C_in zero), then xs [ceil(C_in / (RS*LB)) * RS*LB][BN]
+  // (rows past C_in zero): every staging load and store is unconditional, so
+  // the loads of a batch are all in flight before the first wait.
+  float* ws = smem;
+  float* xs = smem + 256 * 32;
+
+  // weights first (8 float4 per thread), then x in batches of LB independent
+  // loads: thread tid always stages column tid % BN of rows tid / BN + RS * j,
+  // so the bounds test is one comparison per thread.
+  const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(G.w, 4u * (unsigned)(C_in * a.w_ld));
+  const int cols = (a.C_out + 3) & ~3;
+  {
+    const int ci = tid >> 3;
+    const int co = co0 + 4 * (tid & 7);
+    float4 wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = ci + 32 * j;
+      const unsigned off = (c < C_in && co < cols) ? 4u * (unsigned)(c * a.w_ld + co) : kOut;
+      wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) reinterpret_cast<float4*>(ws)[tid + 256 * j] = wv[j];
+  }
+  const __amdgpu_buffer_rsrc_t xrs =
+      uniform_rsrc(G.x + (long long)b * a.xb, 4u * (unsigned)((C_in - 1) * (int)a.xc + a.L_in));
+  const int xcol = tid % BN;
+  const int xrow = tid / BN;
+  const bool xin = i0 + xcol < a.L_in;
+  const int n_it = C_in / RS;  // C_in % 8 == 0, RS <= 8
+  const bool leaky = a.in_act == ACT_LEAKY;
+  for (int j0 = 0; j0 < n_it; j0 += LB) {
+    float v[LB];
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      const int ci = xrow + RS * (j0 + j);
+      const unsigned off = (xin && j0 + j < n_it) ? 4u * (unsigned)(ci * (int)a.xc + i0 + xcol) : kOut;
+      v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      float u = v[j];
+      if (leaky) u = u >= 0.f ? u : u * a.in_slope;
+      xs[(j0 + j) * 256 + tid] = u;
+    }
+  }
+  __syncthreads();
+
+  floatx16 acc[TN];
+#pragma unroll
+  for (int n = 0; n < TN; ++n)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+  // wave w takes input channels [w*q, (w+1)*q), two per MFMA (k = lane / 32)
+  const int q = C_in / 4;
+  const float* wl = ws + (wave * q + half) * 32 + l32;
+  const float* xl = xs + (wave * q + half) * BN + l32;
+  int st = 0;
+  for (; st + 4 <= q / 2; st += 4) {
+    float av[4], bv[4][TN];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      av[u] = wl[2 * (st + u) * 32];
+#pragma unroll
+      for (int n = 0; n < TN; ++n) bv[u][n] = xl[2 * (st + u) * BN + n * 32];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int n = 0; n < TN; ++n) acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u], bv[u][n], acc[n], 0, 0, 0);
+  }
+  for (; st < q / 2; ++st) {
+    const float av = wl[2 * st * 32];
+#pragma unroll
+    for (int n = 0; n < TN; ++n)
+      acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, xl[2 * st * BN + n * 32], acc[n], 0, 0, 0);
+  }
+  __syncthreads();  // the staged operands are dead; the LDS now takes the quarters
+  float* red = smem;  // [wave][n][r][lane]
+#pragma unroll
+  for (int n = 0; n < TN; ++n)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[((wave * TN + n) * 16 + r) * 64 + lane] = acc[n][r];
+  __syncthreads();
+
+  // thread tid forms column i0 + tid % BN of rows tid / BN + RS * k: the four
+  // quarters added in wave order; every global operand is loaded (buffer
+  // loads, masked rows and columns out of range) before the first use, then
+  // v + bias (+ bias2) (+ residual), activation and combine
+  const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
+  float* ob = G.out + (long long)b * a.ob;
+  const float* rb = G.res ? G.res + (long long)b * a.rb : nullptr;
+  const int col = tid % BN;
+  const int i = i0 + col;
+  const int n = col >> 5;
+  const int c32 = col & 31;
+  const bool icol = i < G.n_out;
+  float v[KO];
+  unsigned bo[KO], oo[KO], ro[KO];
+#pragma unroll
+  for (int k = 0; k < KO; ++k) {
+    const int row = tid / BN + k * RS;
+    const int r = (row >> 3) * 4 + (row & 3);
+    const int ln = c32 + 32 * ((row >> 2) & 1);
+    float t = red[((0 * TN + n) * 16 + r) * 64 + ln];
+    t = t + red[((1 * TN + n) * 16 + r) * 64 + ln];
+    t = t + red[((2 * TN + n) * 16 + r) * 64 + ln];
+    v[k] = t + red[((3 * TN + n) * 16 + r) * 64 + ln];
+    const int co = co0 + row;
+    const bool ok = icol && co < a.C_out;
+    bo[k] = ok ? 4u * (unsigned)co : kOut;
+    oo[k] = ok ? 4u * (unsigned)(co * (int)a.oc + i) : kOut;
+    ro[k] = ok ? 4u * (unsigned)(co * (int)a.rc + i) : kOut;
+  }
+  const unsigned o_range = 4u * (unsigned)((a.C_out - 1) * (int)a.oc + G.n_out);
+  const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(ob, o_range);
+  float bv[KO], b2v[KO], rv[KO], ov[KO];
+  if (G.bias) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(G.bias, 4u * (unsigned)a.C_out);
+#pragma unroll
+    for (int k = 0; k < KO; ++k) bv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, bo[k], 0, 0));
+  }
+  if (bias2) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(bias2, 4u * (unsigned)a.C_out);
+#pragma unroll
+    for (int k = 0; k < KO; ++k) b2v[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, bo[k], 0, 0));
+  }
+  if (rb) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(rb, 4u * (unsigned)((a.C_out - 1) * (int)a.rc + G.n_out));
+#pragma unroll
+    for (int k = 0; k < KO; ++k) rv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ro[k], 0, 0));
+  }
+  if (G.combine != COMB_STORE) {
+#pragma unroll
+    for (int k = 0; k < KO; ++k) ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ors, oo[k], 0, 0));
+  }
+#pragma unroll
+  for (int k = 0; k < KO; ++k) {
+    float t = v[k];
+    if (G.bias) t = t + bv[k];
+    if (bias2) t = t + b2v[k];
+    if (rb) t = t + rv[k];
+    t = apply_act(t, a.out_act, a.out_slope);
+    if (G.combine == COMB_ADD) {
+      t = ov[k] + t;
+    } else if (G.combine == COMB_ADD_DIV) {
+      t = (ov[k] + t) / a.div;
+    }
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, t), ors, oo[k], 0, 0);
+  }
+}
+
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
 // added in index order (deterministic), one thread per output element.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(ConvLaunch a) {
@@ -903,9 +1085,54 @@ long long n_blocks(const ConvLaunch& a, int BM, int BN);
 struct SplitPlan {
   int S = 1, csplit = 0, BM = 0;
 };
+// The small 1x1 GEMM path: every group a plain 1x1 conv (no stride, offset or
+// output interleave), at most 256 input channels (the whole reduction fits
+// LDS), a few thousand columns, no reduce post-op.
+bool small_gemm_ok(const ConvLaunch& a) {
+  if (a.C_in > 256 || a.C_in % 8 != 0 || a.post != POST_NONE) return false;
+  for (int g = 0; g < a.n_groups; ++g) {
+    const ConvGroup& G = a.g[g];
+    if (G.K != 1 || G.in_step > 1 || G.in_off != 0 || G.out_step != 1 || G.out_off != 0 || G.n_out > 8192 ||
+        G.n_out > a.L_in)
+      return false;
+  }
+  return true;
+}
+
+bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
+  int n_out = 0;
+  for (int g = 0; g < a.n_groups; ++g) n_out = std::max(n_out, a.g[g].n_out);
+  const int nco = (a.C_out + 31) / 32;
+  const long long z = (long long)a.n_groups * a.B;
+  // 32-bit buffer offsets: x, out and the residual each within 2 GiB of their batch item
+  if (z > 65535 || 4LL * ((a.C_in - 1) * a.xc + a.L_in) >= (1LL << 31) ||
+      4LL * ((a.C_out - 1) * a.oc + n_out) >= (1LL << 31) || 4LL * ((a.C_out - 1) * a.rc + n_out) >= (1LL << 31))
+    return false;
+  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 192;
+  const int BN = wide ? 64 : 32;
+  const size_t n_it = (size_t)a.C_in / (256 / BN);  // staging passes, rounded up to the batch of 16
+  const size_t lds = sizeof(float) * (256 * 32 + (n_it + 15) / 16 * 16 * 256);
+  const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
+  static bool attr = false;
+  if (!attr) {
+    RVC_HIP(hipFuncSetAttribute((const void*)conv1x1_small_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(sizeof(float) * 256 * 96)));
+    RVC_HIP(hipFuncSetAttribute((const void*)conv1x1_small_kernel<32>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(sizeof(float) * 256 * 96)));
+    attr = true;
+  }
+  if (wide)
+    hipLaunchKernelGGL(conv1x1_small_kernel<64>, grid, dim3(256), lds, s, a);
+  else
+    hipLaunchKernelGGL(conv1x1_small_kernel<32>, grid, dim3(256), lds, s, a);
+  check_launch("conv1x1_small");
+  return true;
+}
+
 SplitPlan split_plan(const ConvLaunch& a) {
   SplitPlan p;
   if (a.n_groups != 1 || (a.g[0].in_step > 1) || a.g[0].K < 1) return p;
+  if (small_gemm_ok(a)) return p;  // no split: the small GEMM path takes the whole reduction
   const bool gemm = a.g[0].K == 1;
   int BM = 0, BKT = 0;
   if (a.C_out % 128 == 0) {
@@ -981,6 +1208,7 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
     RVC_CHECK((reinterpret_cast<uintptr_t>(a.g[g].w) & 15) == 0, "conv1d_mfma: weights must be 16-byte aligned");
   }
   if (max_n_out(a) == 0) return;
+  if (step == 1 && small_gemm_ok(a) && launch_small_gemm(a, s)) return;
   // Tile choice: widest co tile that divides C_out while the grid still
   // gives every CU work (256 CUs); few output columns -> split-K waves.
   // The 128 x 128 tile (two resident workgroups per CU) also needs about two

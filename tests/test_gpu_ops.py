@@ -55,6 +55,27 @@ def test_conv1d_small_vs_loops(ops, B, C, O, T, K, pl, pr, d):
     assert rel_l2(got, loops.conv1d(x, w, b, 1, pl, pr, d)) < TOL
 
 
+@pytest.mark.parametrize("B,C,O,T", [
+    (1, 192, 576, 1000),   # enc_p q/k/v at config 2
+    (1, 192, 192, 1000),   # conv_o, flow res/skip
+    (2, 96, 192, 37),      # flow pre, ragged length, batch 2
+    (1, 192, 96, 1000),    # flow post (C_out not a multiple of 64)
+    (1, 256, 48, 300),     # widest staged reduction, C_out not a multiple of 32
+    (1, 24, 40, 4097),     # narrow reduction, one column past a tile edge
+])
+def test_conv1d_1x1_small_gemm(ops, B, C, O, T):
+    """Plain 1x1 convs at a few thousand columns run the whole-reduction LDS
+    kernel (C_in <= 256): against the oracle at rel L2 1e-4 and, on tiny
+    slices, the float64 loops."""
+    rng = np.random.default_rng(B * 1000 + C + O)
+    x, w, b = _r(rng, B, C, T), _r(rng, O, C, 1, scale=C ** -0.5), _r(rng, O)
+    got = ops.conv1d(x, w, b)
+    assert got.shape == (B, O, T)
+    assert rel_l2(got, nn.conv1d(x, w, b)) < TOL
+    sl = loops.conv1d(x[:, :, :7], w, b)
+    assert rel_l2(got[:, :, :7], sl) < TOL
+
+
 RESBLOCK = [(C, L, k, d) for C, L in ((256, 1024), (128, 2048), (64, 4096), (32, 8192))
             for k in (3, 7, 11) for d in (1, 3, 5)]
 
