@@ -125,6 +125,79 @@ __global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
   *o = v;
 }
 
+// Single-input-channel convolutions at dilation 1 (the NSF noise convs of
+// the decoder stages the ConvTranspose epilogue does not cover: 1 -> C with
+// k = 2 * stride, runtime/models/vits.py:1628-1635).  A workgroup owns
+// kC1Out outputs x kC1Co channels.  The input window is staged phase-major,
+// xs[r][m] = x[t0 + m * stride + r], so output j's tap k reads
+// xs[k % stride][j + k / stride] and a wave's 32 neighbouring outputs read
+// 32 consecutive LDS words; the weights are staged [k][32 channels] and read
+// as float4 broadcasts.  Thread t forms outputs t % 32 + 32u (u < 4) of
+// channels 4 * (t / 32) .. +3, the taps summed in order.
+constexpr int kC1Out = 128, kC1Co = 32;
+size_t c1_lds_floats(int K, int stride) {
+  const int M = kC1Out + (K - 1) / stride + 1;
+  return (size_t)K * kC1Co + (size_t)stride * M;
+}
+__global__ __launch_bounds__(256) void conv1d_c1_kernel(DirectConvArgs a) {
+  extern __shared__ float sm[];
+  const int i0 = blockIdx.x * kC1Out, co0 = blockIdx.y * kC1Co, b = blockIdx.z;
+  const int S = a.stride, K = a.K;
+  const int M = kC1Out + (K - 1) / S + 1;  // columns per phase row
+  float* ws = sm;                          // [K][kC1Co]
+  float* xs = sm + K * kC1Co;              // [S][M]
+  const int tid = threadIdx.x;
+  for (int e = tid; e < K * kC1Co; e += 256) {
+    const int k = e / kC1Co, c = e - k * kC1Co;
+    const int co = co0 + c;
+    ws[e] = co < a.C_out ? a.w[(long long)co * K + k] : 0.f;
+  }
+  const float* xb = a.x + (long long)b * a.xb;
+  const long long tb = (long long)i0 * S + a.in_off;
+  for (int q = tid; q < S * M; q += 256) {  // global order: coalesced reads
+    const int m = q / S, r = q - m * S;
+    const long long t = tb + q;
+    xs[r * M + m] = (t >= 0 && t < a.L_in) ? act_in(xb[t], a.in_act, a.in_slope) : 0.f;
+  }
+  __syncthreads();
+  const int jl = tid & 31, cq = tid >> 5;
+  float acc[4][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[u][c] = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float4 wv = *reinterpret_cast<const float4*>(ws + k * kC1Co + 4 * cq);
+    const float* xr = xs + (k % S) * M + k / S + jl;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float xv = xr[32 * u];
+      acc[u][0] += wv.x * xv;
+      acc[u][1] += wv.y * xv;
+      acc[u][2] += wv.z * xv;
+      acc[u][3] += wv.w * xv;
+    }
+  }
+  float* ob = a.out + (long long)b * a.ob;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int co = co0 + 4 * cq + c;
+    if (co >= a.C_out) break;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + jl + 32 * u;
+      if (i >= a.n_out) continue;
+      float v = acc[u][c];
+      if (a.bias) v = v + a.bias[co];
+      v = act_out(v, a.out_act, a.out_slope);
+      float* o = ob + (long long)co * a.oc + i;
+      if (a.combine == COMB_ADD) v = *o + v;
+      else if (a.combine == COMB_ADD_DIV) v = (*o + v) / a.div;
+      *o = v;
+    }
+  }
+}
+
 // Gather-form ConvTranspose1d: one thread per output element.
 __global__ __launch_bounds__(256) void conv_t1d_direct_kernel(ConvTArgs a) {
   const long long n = (long long)a.B * a.C_out * a.n_out;
@@ -216,7 +289,11 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
   RVC_CHECK(!a.x2 || (a.x3 && a.C_out < 8 && a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax),
             "conv1d_direct: a three-input average needs the stride-1 row kernel");
   if (a.n_out <= 0) return;
-  if (a.C_out >= 8) {
+  if (a.C_in == 1 && a.dil == 1 && !a.x2 && a.C_out >= 8 && a.stride <= 64 &&
+      c1_lds_floats(a.K, a.stride) * sizeof(float) <= 65536) {
+    dim3 grid((a.n_out + kC1Out - 1) / kC1Out, (a.C_out + kC1Co - 1) / kC1Co, a.B);
+    hipLaunchKernelGGL(conv1d_c1_kernel, grid, dim3(256), c1_lds_floats(a.K, a.stride) * sizeof(float), s, a);
+  } else if (a.C_out >= 8) {
     dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);
     hipLaunchKernelGGL(conv1d_direct_kernel<8>, grid, dim3(256), 0, s, a);
   } else if (a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax) {

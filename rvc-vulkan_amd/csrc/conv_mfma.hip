@@ -708,20 +708,128 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
 }
 
 // ---------------------------------------------------------------------------
-// Small 1x1 GEMMs (enc_p / flow projections at a few thousand frames): the
-// whole reduction of a 32 x BN output tile -- x[0:C_in][i0:i0+BN] and
-// W[0:C_in][co0:co0+32], C_in <= 256 -- is staged into LDS with one round of
-// loads, the four waves each take a quarter of the input channels for the
+// Small convolutions (enc_p / flow at a few thousand frames).  One workgroup
+// forms a 32 x BN output tile over the WHOLE reduction: its four waves each
+// take a quarter of the input channels of every staged chunk, accumulate the
 // full tile, and the quarters are added through LDS in wave order
-// (((q0 + q1) + q2) + q3), then + bias (+ bias2) (+ residual), activation
-// and combine, in the split-K reduce's order.  One launch, one load latency
-// and no partial-sum tensor, where the chunked kernel pays a load round trip
-// per channel chunk and a separate reduce.
+// (((q0 + q1) + q2) + q3) -- one launch and no partial-sum tensor, where the
+// split-K path writes and re-reads every split's partial tile.
+
+// The shared epilogue: each wave stores its 32 x BN accumulators to red
+// [wave][n][r][lane], then thread tid forms column i0 + tid % BN of tile rows
+// tid / BN + RS * k.  Every global operand is loaded (buffer loads, rows and
+// columns out of range masked to the out-of-range offset) before the first
+// use.  Plain: out = combine(act(v + bias (+ bias2) (+ residual))), the
+// split-K reduce's order.  WaveNet gate (gate = true): tile rows [0, 16) are
+// channels cb + r, rows [16, 32) channels H + cb + r - 16, and
+// out[c] = tanh(v_c + g_c) * sigmoid(v_{H+c} + g_{H+c}) for the 16 channels
+// (v including the bias), g per batch item.
+template <int BN>
+__device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const ConvGroup& G, int b, int i0, int co0,
+                                                    bool gate, const floatx16 (&acc)[BN / 32], float* red) {
+  constexpr int TN = BN / 32;
+  constexpr int RS = 256 / BN;
+  constexpr int KO = 32 * BN / 256;
+  constexpr unsigned kOut = 0x80000000u;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  __syncthreads();  // the staged operands are dead; the LDS now takes the quarters
+#pragma unroll
+  for (int n = 0; n < TN; ++n)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[((wave * TN + n) * 16 + r) * 64 + lane] = acc[n][r];
+  __syncthreads();
+
+  const int H = a.post_H;
+  const int col = tid % BN;
+  const int i = i0 + col;
+  const int n = col >> 5;
+  const int c32 = col & 31;
+  const bool icol = i < G.n_out;
+  float v[KO];
+  unsigned bo[KO], oo[KO], ro[KO];
+#pragma unroll
+  for (int k = 0; k < KO; ++k) {
+    const int row = tid / BN + k * RS;
+    const int r = (row >> 3) * 4 + (row & 3);
+    const int ln = c32 + 32 * ((row >> 2) & 1);
+    float t = red[((0 * TN + n) * 16 + r) * 64 + ln];
+    t = t + red[((1 * TN + n) * 16 + r) * 64 + ln];
+    t = t + red[((2 * TN + n) * 16 + r) * 64 + ln];
+    v[k] = t + red[((3 * TN + n) * 16 + r) * 64 + ln];
+    const int co = gate ? (row < 16 ? co0 + row : H + co0 + row - 16) : co0 + row;
+    const bool ok = icol && co < a.C_out;
+    bo[k] = ok ? 4u * (unsigned)co : kOut;
+    oo[k] = ok ? 4u * (unsigned)(co * (int)a.oc + i) : kOut;
+    ro[k] = ok ? 4u * (unsigned)(co * (int)a.rc + i) : kOut;
+  }
+  float bv[KO];
+  if (G.bias) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(G.bias, 4u * (unsigned)a.C_out);
+#pragma unroll
+    for (int k = 0; k < KO; ++k) bv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, bo[k], 0, 0));
+  }
+  float* ob = G.out + (long long)b * a.ob;
+  if (gate) {
+    // rows k < KO / 2 are the tanh channels, rows k + KO / 2 their sigmoid partners
+    const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(ob, 4u * (unsigned)((H - 1) * (int)a.oc + G.n_out));
+    const __amdgpu_buffer_rsrc_t grs = uniform_rsrc(a.post_g + (long long)b * a.post_gb, 8u * (unsigned)H);
+    float gv[KO];
+#pragma unroll
+    for (int k = 0; k < KO; ++k) gv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(grs, bo[k], 0, 0));
+#pragma unroll
+    for (int k = 0; k < KO / 2; ++k) {
+      float v1 = v[k], v2 = v[k + KO / 2];
+      if (G.bias) {
+        v1 = v1 + bv[k];
+        v2 = v2 + bv[k + KO / 2];
+      }
+      const float t = tanhf(v1 + gv[k]) * sigmoid_as(v2 + gv[k + KO / 2]);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, t), ors, oo[k], 0, 0);
+    }
+    return;
+  }
+  const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
+  const float* rb = G.res ? G.res + (long long)b * a.rb : nullptr;
+  const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(ob, 4u * (unsigned)((a.C_out - 1) * (int)a.oc + G.n_out));
+  float b2v[KO], rv[KO], ov[KO];
+  if (bias2) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(bias2, 4u * (unsigned)a.C_out);
+#pragma unroll
+    for (int k = 0; k < KO; ++k) b2v[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, bo[k], 0, 0));
+  }
+  if (rb) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(rb, 4u * (unsigned)((a.C_out - 1) * (int)a.rc + G.n_out));
+#pragma unroll
+    for (int k = 0; k < KO; ++k) rv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ro[k], 0, 0));
+  }
+  if (G.combine != COMB_STORE) {
+#pragma unroll
+    for (int k = 0; k < KO; ++k) ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ors, oo[k], 0, 0));
+  }
+#pragma unroll
+  for (int k = 0; k < KO; ++k) {
+    float t = v[k];
+    if (G.bias) t = t + bv[k];
+    if (bias2) t = t + b2v[k];
+    if (rb) t = t + rv[k];
+    t = apply_act(t, a.out_act, a.out_slope);
+    if (G.combine == COMB_ADD) {
+      t = ov[k] + t;
+    } else if (G.combine == COMB_ADD_DIV) {
+      t = (ov[k] + t) / a.div;
+    }
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, t), ors, oo[k], 0, 0);
+  }
+}
+
+// 1x1 convs, C_in <= 256: the whole reduction -- x[0:C_in][i0:i0+BN] and
+// W[0:C_in][co0:co0+32] -- staged into LDS with one round of loads.
 template <int BN>
 __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
   constexpr int TN = BN / 32;
   constexpr int RS = 256 / BN;        // input channels one pass of the workgroup stages
-  constexpr int KO = 32 * BN / 256;   // outputs each thread forms
   constexpr int LB = 16;              // loads in flight per thread per staging batch
   constexpr unsigned kOut = 0x80000000u;
   extern __shared__ float smem[];
@@ -814,79 +922,117 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
     for (int n = 0; n < TN; ++n)
       acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, xl[2 * st * BN + n * 32], acc[n], 0, 0, 0);
   }
-  __syncthreads();  // the staged operands are dead; the LDS now takes the quarters
-  float* red = smem;  // [wave][n][r][lane]
+  small_conv_epilogue<BN>(a, G, b, i0, co0, false, acc, smem);
+}
+
+// K-tap convs (K = 3 or 5, dilation 1, stride 1), C_in % CHK == 0: the
+// reduction streams through LDS in chunks of CHK input channels with all K
+// taps -- W[0:K][c0:c0+CHK][32 rows] and x[c0:c0+CHK][i0+in_off : +BN+K-1] --
+// the next chunk's loads in flight (registers) while the current one is
+// multiplied.  Wave w takes channels [w*CHK/4, (w+1)*CHK/4) of every chunk,
+// two per MFMA (k = lane / 32), the K taps innermost.  POST_WN_GATE launches
+// map tile rows to channel pairs (16 tanh channels and their sigmoid
+// partners, cb = blockIdx.y * 16).
+template <int BN, int K, int CHK>
+__global__ __launch_bounds__(256) void conv_small_kernel(ConvLaunch a) {
+  constexpr int TN = BN / 32;
+  constexpr int XW = BN + K - 1;             // staged input columns per channel
+  constexpr int WF4 = K * CHK / 32;          // float4 weight loads per thread per chunk
+  constexpr int XE = (CHK * XW + 255) / 256; // input loads per thread per chunk
+  constexpr unsigned kOut = 0x80000000u;
+  extern __shared__ float smem[];
+  float* ws = smem;                // [K][CHK][32]
+  float* xs = smem + K * CHK * 32; // [XE * 256] (CHK rows of XW, tail unused)
+  const int b = blockIdx.z % a.B;
+  const int gi = blockIdx.z / a.B;
+  const ConvGroup& G = a.g[gi];
+  const int i0 = blockIdx.x * BN;
+  if (i0 >= G.n_out) return;  // uniform for the whole workgroup, before any barrier
+  const bool gate = a.post == POST_WN_GATE;
+  const int co0 = gate ? blockIdx.y * 16 : blockIdx.y * 32;
+  const int H = a.post_H;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int C_in = a.C_in;
+  const int n_ch = C_in / CHK;
+
+  const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(G.w, 4u * (unsigned)(K * C_in * a.w_ld));
+  const __amdgpu_buffer_rsrc_t xrs =
+      uniform_rsrc(G.x + (long long)b * a.xb, 4u * (unsigned)((C_in - 1) * (int)a.xc + a.L_in));
+  // per-thread staging offsets relative to the chunk's first channel
+  const int cols = (a.C_out + 3) & ~3;
+  unsigned wo[WF4];
+#pragma unroll
+  for (int j = 0; j < WF4; ++j) {
+    const int f = j * 256 + tid;  // float4 index in [K][CHK][8]
+    const int kc = f >> 3;
+    const int k = kc / CHK, ci = kc - k * CHK;
+    const int r4 = 4 * (f & 7);
+    const int co = gate ? (r4 < 16 ? co0 + r4 : H + co0 + r4 - 16) : co0 + r4;
+    wo[j] = co < cols ? 4u * (unsigned)((k * C_in + ci) * a.w_ld + co) : kOut;
+  }
+  unsigned xo[XE];
+#pragma unroll
+  for (int j = 0; j < XE; ++j) {
+    const int e = j * 256 + tid;
+    const int ci = e / XW;
+    const int t = i0 + G.in_off + (e - ci * XW);
+    xo[j] = (e < CHK * XW && t >= 0 && t < a.L_in) ? 4u * (unsigned)(ci * (int)a.xc + t) : kOut;
+  }
+  float4 wv[WF4];
+  float xv[XE];
+  auto load = [&](int c) {
+    const unsigned wadd = 4u * (unsigned)(c * CHK * a.w_ld);
+    const unsigned xadd = 4u * (unsigned)(c * CHK * (int)a.xc);
+#pragma unroll
+    for (int j = 0; j < WF4; ++j)
+      wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wo[j] == kOut ? kOut : wo[j] + wadd, 0, 0));
+#pragma unroll
+    for (int j = 0; j < XE; ++j)
+      xv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xo[j] == kOut ? kOut : xo[j] + xadd, 0, 0));
+  };
+  const bool leaky = a.in_act == ACT_LEAKY;
+
+  floatx16 acc[TN];
 #pragma unroll
   for (int n = 0; n < TN; ++n)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[((wave * TN + n) * 16 + r) * 64 + lane] = acc[n][r];
-  __syncthreads();
-
-  // thread tid forms column i0 + tid % BN of rows tid / BN + RS * k: the four
-  // quarters added in wave order; every global operand is loaded (buffer
-  // loads, masked rows and columns out of range) before the first use, then
-  // v + bias (+ bias2) (+ residual), activation and combine
-  const float* bias2 = a.bias2 ? a.bias2 + (long long)b * a.bias2b : nullptr;
-  float* ob = G.out + (long long)b * a.ob;
-  const float* rb = G.res ? G.res + (long long)b * a.rb : nullptr;
-  const int col = tid % BN;
-  const int i = i0 + col;
-  const int n = col >> 5;
-  const int c32 = col & 31;
-  const bool icol = i < G.n_out;
-  float v[KO];
-  unsigned bo[KO], oo[KO], ro[KO];
+    for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+  constexpr int Q = CHK / 4;
+  const float* wl = ws + (wave * Q + half) * 32 + l32;
+  const float* xl = xs + (wave * Q + half) * XW + l32;
+  load(0);
+  for (int c = 0; c < n_ch; ++c) {
 #pragma unroll
-  for (int k = 0; k < KO; ++k) {
-    const int row = tid / BN + k * RS;
-    const int r = (row >> 3) * 4 + (row & 3);
-    const int ln = c32 + 32 * ((row >> 2) & 1);
-    float t = red[((0 * TN + n) * 16 + r) * 64 + ln];
-    t = t + red[((1 * TN + n) * 16 + r) * 64 + ln];
-    t = t + red[((2 * TN + n) * 16 + r) * 64 + ln];
-    v[k] = t + red[((3 * TN + n) * 16 + r) * 64 + ln];
-    const int co = co0 + row;
-    const bool ok = icol && co < a.C_out;
-    bo[k] = ok ? 4u * (unsigned)co : kOut;
-    oo[k] = ok ? 4u * (unsigned)(co * (int)a.oc + i) : kOut;
-    ro[k] = ok ? 4u * (unsigned)(co * (int)a.rc + i) : kOut;
-  }
-  const unsigned o_range = 4u * (unsigned)((a.C_out - 1) * (int)a.oc + G.n_out);
-  const __amdgpu_buffer_rsrc_t ors = uniform_rsrc(ob, o_range);
-  float bv[KO], b2v[KO], rv[KO], ov[KO];
-  if (G.bias) {
-    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(G.bias, 4u * (unsigned)a.C_out);
+    for (int j = 0; j < WF4; ++j) reinterpret_cast<float4*>(ws)[j * 256 + tid] = wv[j];
 #pragma unroll
-    for (int k = 0; k < KO; ++k) bv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, bo[k], 0, 0));
-  }
-  if (bias2) {
-    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(bias2, 4u * (unsigned)a.C_out);
-#pragma unroll
-    for (int k = 0; k < KO; ++k) b2v[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, bo[k], 0, 0));
-  }
-  if (rb) {
-    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(rb, 4u * (unsigned)((a.C_out - 1) * (int)a.rc + G.n_out));
-#pragma unroll
-    for (int k = 0; k < KO; ++k) rv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ro[k], 0, 0));
-  }
-  if (G.combine != COMB_STORE) {
-#pragma unroll
-    for (int k = 0; k < KO; ++k) ov[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ors, oo[k], 0, 0));
-  }
-#pragma unroll
-  for (int k = 0; k < KO; ++k) {
-    float t = v[k];
-    if (G.bias) t = t + bv[k];
-    if (bias2) t = t + b2v[k];
-    if (rb) t = t + rv[k];
-    t = apply_act(t, a.out_act, a.out_slope);
-    if (G.combine == COMB_ADD) {
-      t = ov[k] + t;
-    } else if (G.combine == COMB_ADD_DIV) {
-      t = (ov[k] + t) / a.div;
+    for (int j = 0; j < XE; ++j) {
+      float u = xv[j];
+      if (leaky) u = u >= 0.f ? u : u * a.in_slope;
+      xs[j * 256 + tid] = u;
     }
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, t), ors, oo[k], 0, 0);
+    __syncthreads();
+    if (c + 1 < n_ch) load(c + 1);
+#pragma unroll 2
+    for (int st = 0; st < Q / 2; ++st) {
+      float av[K], bv[K][TN];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        av[k] = wl[(k * CHK + 2 * st) * 32];
+#pragma unroll
+        for (int n = 0; n < TN; ++n) bv[k][n] = xl[2 * st * XW + n * 32 + k];
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+#pragma unroll
+        for (int n = 0; n < TN; ++n) acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[k], bv[k][n], acc[n], 0, 0, 0);
+    }
+    if (c + 1 < n_ch) __syncthreads();  // the next chunk's stores overwrite this one
   }
+  small_conv_epilogue<BN>(a, G, b, i0, co0, gate, acc, smem);
 }
 
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
@@ -1099,6 +1245,80 @@ bool small_gemm_ok(const ConvLaunch& a) {
   return true;
 }
 
+// The chunked path: K = 3 or 5 at dilation 1 in every group (C_in a multiple
+// of 64 up to 1024), or 1x1 GEMMs too wide for the whole-reduction kernel
+// (C_in a multiple of 128 up to 4096); stride 1, a few thousand columns and a
+// tile grid too small to fill the GPU (where the split-K path would run); the
+// reduce post-op POST_WN_GATE when C_out = 2 * post_H with post_H % 16 == 0.
+bool small_conv_ok(const ConvLaunch& a) {
+  const int K = a.g[0].K;
+  if (K == 1 ? (a.C_in % 128 != 0 || a.C_in > 4096) : (a.C_in % 64 != 0 || a.C_in > 1024)) return false;
+  if (a.post == POST_WN_GATE) {
+    if (a.n_groups != 1 || a.post_H % 16 != 0 || a.C_out != 2 * a.post_H) return false;
+  } else if (a.post != POST_NONE) {
+    return false;
+  }
+  if (K != 1 && K != 3 && K != 5) return false;
+  for (int g = 0; g < a.n_groups; ++g) {
+    const ConvGroup& G = a.g[g];
+    if (G.K != K || G.dil != 1 || G.in_step > 1 || G.out_step != 1 || G.out_off != 0 || G.n_out > 8192 ||
+        G.in_off > 0 || G.in_off < -(K - 1))
+      return false;
+  }
+  return n_blocks(a, 64, 128) < 384;
+}
+
+template <int BN, int K, int CHK>
+void launch_small_conv_cfg(const ConvLaunch& a, dim3 grid, hipStream_t s) {
+  constexpr int XE = (CHK * (BN + K - 1) + 255) / 256;
+  constexpr size_t lds = sizeof(float) * ((size_t)K * CHK * 32 + (size_t)XE * 256);
+  static_assert(lds >= sizeof(float) * 4 * (BN / 32) * 16 * 64, "the epilogue's reduction must fit the staging LDS");
+  static_assert(lds <= 160 * 1024, "staging LDS above the CU's 160 KiB");
+  if (lds > 65536) {
+    static bool attr = false;  // per instantiation
+    if (!attr) {
+      RVC_HIP(hipFuncSetAttribute((const void*)conv_small_kernel<BN, K, CHK>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+      attr = true;
+    }
+  }
+  hipLaunchKernelGGL((conv_small_kernel<BN, K, CHK>), grid, dim3(256), lds, s, a);
+}
+
+bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
+  const int n_out = max_n_out(a);
+  const bool gate = a.post == POST_WN_GATE;
+  RVC_CHECK(!gate || a.post_g, "conv1d_mfma: the WaveNet gate needs its conditioning vector");
+  const int nco = gate ? a.post_H / 16 : (a.C_out + 31) / 32;
+  const long long z = (long long)a.n_groups * a.B;
+  const int K = a.g[0].K;
+  // 32-bit buffer offsets: x, the weights, out and the residual within 2 GiB
+  if (z > 65535 || 4LL * ((a.C_in - 1) * a.xc + a.L_in) >= (1LL << 31) ||
+      4LL * K * a.C_in * a.w_ld >= (1LL << 31) || 4LL * ((a.C_out - 1) * a.oc + n_out) >= (1LL << 31) ||
+      4LL * ((a.C_out - 1) * a.rc + n_out) >= (1LL << 31))
+    return false;
+  // 64-column tiles while they give ~256 workgroups, else 32 (the reduction
+  // order does not depend on the tile width or the batch)
+  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 192;
+  const int BN = wide ? 64 : 32;
+  // 128-channel chunks for the long 3-tap reductions (enc_p's FFN output
+  // conv, C_in = 768): half the chunk round trips
+  const int CHK = K == 3 && a.C_in % 128 == 0 && a.C_in >= 512 ? 128 : 64;
+  const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
+  if (K == 1) {
+    wide ? launch_small_conv_cfg<64, 1, 128>(a, grid, s) : launch_small_conv_cfg<32, 1, 128>(a, grid, s);
+  } else if (K == 3) {
+    if (CHK == 128)
+      wide ? launch_small_conv_cfg<64, 3, 128>(a, grid, s) : launch_small_conv_cfg<32, 3, 128>(a, grid, s);
+    else
+      wide ? launch_small_conv_cfg<64, 3, 64>(a, grid, s) : launch_small_conv_cfg<32, 3, 64>(a, grid, s);
+  } else {
+    wide ? launch_small_conv_cfg<64, 5, 64>(a, grid, s) : launch_small_conv_cfg<32, 5, 64>(a, grid, s);
+  }
+  check_launch("conv_small");
+  return true;
+}
+
 bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
   int n_out = 0;
   for (int g = 0; g < a.n_groups; ++g) n_out = std::max(n_out, a.g[g].n_out);
@@ -1132,7 +1352,7 @@ bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
 SplitPlan split_plan(const ConvLaunch& a) {
   SplitPlan p;
   if (a.n_groups != 1 || (a.g[0].in_step > 1) || a.g[0].K < 1) return p;
-  if (small_gemm_ok(a)) return p;  // no split: the small GEMM path takes the whole reduction
+  if (small_gemm_ok(a) || small_conv_ok(a)) return p;  // no split: a small-conv kernel takes the whole reduction
   const bool gemm = a.g[0].K == 1;
   int BM = 0, BKT = 0;
   if (a.C_out % 128 == 0) {
@@ -1185,6 +1405,13 @@ void launch_splitk_reduce(const ConvLaunch& a, hipStream_t s) {
   check_launch("splitk_reduce");
 }
 
+bool conv1d_mfma_fuses_gate(const ConvLaunch& a) {
+  ConvLaunch t = a;
+  t.post = POST_WN_GATE;
+  t.post_H = a.C_out / 2;
+  return (a.C_out % 2 == 0 && small_conv_ok(t)) || split_plan(t).S > 1;
+}
+
 size_t conv1d_mfma_split_floats(const ConvLaunch& a) {
   const SplitPlan p = split_plan(a);
   return p.S > 1 ? (size_t)p.S * a.B * a.C_out * a.g[0].n_out : 0;
@@ -1200,7 +1427,8 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
             "conv1d_mfma: invalid shape");
   const int step = a.g[0].in_step <= 1 ? 1 : a.g[0].in_step;
   RVC_CHECK(step == 1 || step == 2, "conv1d_mfma: input stride must be 1 or 2");
-  RVC_CHECK(a.post == POST_NONE || (a.n_groups == 1 && step == 1 && a.part), "conv1d_mfma: a reduce post-op needs the split-K path");
+  RVC_CHECK(a.post == POST_NONE || (a.n_groups == 1 && step == 1 && (a.part || small_conv_ok(a))),
+            "conv1d_mfma: a reduce post-op needs the split-K or the small-conv path");
   for (int g = 0; g < a.n_groups; ++g) {
     RVC_CHECK(a.g[g].n_out >= 0 && conv1d_mfma_supported(a.g[g].K, a.g[g].dil),
               "conv1d_mfma: taps / dilation outside the MFMA path");
@@ -1209,6 +1437,7 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   }
   if (max_n_out(a) == 0) return;
   if (step == 1 && small_gemm_ok(a) && launch_small_gemm(a, s)) return;
+  if (step == 1 && small_conv_ok(a) && launch_small_conv(a, s)) return;
   // Tile choice: widest co tile that divides C_out while the grid still
   // gives every CU work (256 CUs); few output columns -> split-K waves.
   // The 128 x 128 tile (two resident workgroups per CU) also needs about two
@@ -1239,7 +1468,7 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
       if (ok) return;
     }
   }
-  RVC_CHECK(a.post == POST_NONE, "conv1d_mfma: a reduce post-op needs the split-K path");
+  RVC_CHECK(a.post == POST_NONE, "conv1d_mfma: a reduce post-op needs the split-K or the small-conv path");
   int kmax = 0;
   for (int g = 0; g < a.n_groups; ++g) kmax = std::max(kmax, a.g[g].K);
   if (kmax == 1) {  // 1x1 convolutions: plain GEMMs with 32-channel chunks

@@ -118,8 +118,9 @@ struct ConvLaunch {
   float* part;
   size_t part_floats;
   int ksplit, csplit;  // set by the launcher
-  // what the split-K reduce does with v = sum of the splits + bias (the
-  // launch must take the split path: conv1d_mfma_split_floats(a) > 0):
+  // what the split-K reduce (or the small-conv kernel) does with v = sum of
+  // the splits + bias (the launch must take one of those paths:
+  // conv1d_mfma_fuses_gate(a) for the gate):
   //   POST_WN_GATE   (C_out = 2H): out[c][t] = tanh(v_c + g[c]) * sig(v_{H+c} + g[H+c])
   //                  for c < H, out of row stride oc, g per batch item (stride post_gb)
   //   POST_WN_UPDATE (C_out = 2H, or H when post_last): h += v_c (c < H, not last),
@@ -140,6 +141,10 @@ enum Post : int { POST_NONE = 0, POST_WN_GATE = 1, POST_WN_UPDATE = 2 };
 bool conv1d_mfma_supported(int K, int dil);
 // Scratch floats a launch needs for split-K partial sums (0: no split).
 size_t conv1d_mfma_split_floats(const ConvLaunch& a);
+// Whether the launch, given post = POST_WN_GATE (post_H = C_out / 2), takes a
+// path that applies the gate (split-K reduce or the small-conv kernel); the
+// caller adds a separate gate launch otherwise.
+bool conv1d_mfma_fuses_gate(const ConvLaunch& a);
 void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s);
 // out = combine(act(sum of the split-K partials + bias ...)) for a launch
 // with a.ksplit > 1 (shared by the fp32 and bf16 kernels)

@@ -435,12 +435,12 @@ struct Synth : SessionBase {
       run("flow.glue", 2.0 * B * gin * 2.0 * H * kWnLayers, 4.0 * (B * gin + (double)(gin + 1 + B) * 2 * H * kWnLayers),
           [&] { launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s); });
       for (int i = 0; i < kWnLayers; ++i) {
-        // in-layer conv + gate: fused into the split-K reduce when the conv
-        // takes the split path (it does at P <= ~2000), a separate
-        // elementwise launch otherwise
+        // in-layer conv + gate: fused into the small-conv kernel's epilogue
+        // or the split-K reduce when the conv takes one of those paths (it
+        // does at P <= ~8000), a separate elementwise launch otherwise
         ConvLaunch ci = cargs_same(h, HP, P, L.in_w[i], L.in_b[i], xi, 2 * HP, P, B, H, 2 * H, P, kWnKernel, 1,
                                    (kWnKernel - 1) / 2);
-        if (conv1d_mfma_split_floats(ci) > 0) {
+        if (conv1d_mfma_fuses_gate(ci)) {
           ci.post = POST_WN_GATE;
           ci.post_g = gv + (long long)i * 2 * H;
           ci.post_gb = (long long)2 * H * kWnLayers;
@@ -458,10 +458,11 @@ struct Synth : SessionBase {
         // res/skip conv as one launch of two output groups over the same
         // input: rows [0, H) accumulate into h (h += rs[:H]), rows [H, 2H)
         // into skip (skip = rs[H:] on the first layer); the last layer has
-        // only the skip rows.  An accumulating group starts its accumulators
-        // at (bias + current value) and adds the conv sum to that, i.e.
-        // (b + h) + sum where the reference forms h + (sum + b): the same
-        // terms in another float32 order.
+        // only the skip rows.  Up to 8192 frames the launch runs the
+        // whole-reduction 1x1 kernel, which forms h + (sum + b) as the
+        // reference does; longer sequences take the one-shot tiled kernel,
+        // whose accumulating groups start at (b + h) and add the sum: the
+        // same terms in another float32 order.
         const bool has_h = i + 1 < kWnLayers;
         ConvLaunch cr = c1x1(acts, HP, L.rs_w[i], L.rs_b[i], has_h ? h : skip, B, H, H, P);
         cr.w_ld = packed_ld(L.rs_out[i]);

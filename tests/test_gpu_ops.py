@@ -76,6 +76,32 @@ def test_conv1d_1x1_small_gemm(ops, B, C, O, T):
     assert rel_l2(got[:, :, :7], sl) < TOL
 
 
+@pytest.mark.parametrize("B,C,O,T,K,pad", [
+    (1, 192, 768, 1000, 3, 1),   # enc_p FFN input conv at config 2
+    (1, 768, 192, 1000, 3, 1),   # FFN output conv (128-channel chunks)
+    (2, 192, 384, 1000, 5, 2),   # flow WaveNet in-layer shape, batch 2
+    (1, 192, 384, 37, 5, 2),     # ragged length, one column tile
+    (1, 64, 32, 300, 3, (2, 0)), # left padding only
+    (1, 128, 100, 777, 5, 2),    # C_out not a multiple of 32
+    (1, 512, 256, 130, 3, 1),    # 128-channel chunks at the smallest C_in
+    (1, 768, 192, 1000, 1, 0),   # enc_p phone embedding
+    (2, 768, 2304, 499, 1, 0),   # HuBERT qkv at 10 s, batch 2
+    (1, 3072, 768, 499, 1, 0),   # HuBERT FFN output
+])
+def test_conv1d_small_chunked(ops, B, C, O, T, K, pad):
+    """K = 3 / 5 convs and wide 1x1 GEMMs on short sequences run the chunked
+    whole-reduction kernel (no split-K): against the oracle at rel L2 1e-4,
+    the first columns also against the float64 loops."""
+    rng = np.random.default_rng(B * 7 + C + O + T)
+    x, w, b = _r(rng, B, C, T), _r(rng, O, C, K, scale=(C * K) ** -0.5), _r(rng, O)
+    got = ops.conv1d(x, w, b, padding=pad)
+    pl, pr = (pad, pad) if isinstance(pad, int) else pad
+    assert got.shape == (B, O, T + pl + pr - K + 1)
+    assert rel_l2(got, nn.conv1d(x, w, b, 1, (pl, pr))) < TOL
+    sl = loops.conv1d(x[:, :, :9], w, b, 1, pl, 0)
+    assert rel_l2(got[:, :, :sl.shape[-1]], sl) < TOL
+
+
 RESBLOCK = [(C, L, k, d) for C, L in ((256, 1024), (128, 2048), (64, 4096), (32, 8192))
             for k in (3, 7, 11) for d in (1, 3, 5)]
 
@@ -136,11 +162,17 @@ def test_conv1d_encoder_flow_shapes(ops, C_in, C_out, L, K):
     assert rel_l2(got, nn.conv1d(x, w, b, padding=(K - 1) // 2)) < TOL
 
 
-@pytest.mark.parametrize("C_out,k,s", [(256, 80, 40), (128, 8, 4), (64, 4, 2), (32, 1, 1)])
-def test_conv1d_noise_conv_shapes(ops, C_out, k, s):
+@pytest.mark.parametrize("C_out,k,s,B,L", [
+    (256, 80, 40, 1, 64 * 40), (128, 8, 4, 1, 64 * 40), (64, 4, 2, 1, 64 * 40), (32, 1, 1, 1, 64 * 40),
+    (256, 80, 40, 2, 1000 * 40 + 17),  # config-2 stage 0, batch 2, a ragged last tile
+    (20, 7, 3, 1, 3001),               # channels and taps not multiples of the tile
+    (256, 64, 32, 1, 777 * 32),        # 32 kHz stage 0
+])
+def test_conv1d_noise_conv_shapes(ops, C_out, k, s, B, L):
+    """Single-input-channel strided convs (the NSF noise convs) against the
+    oracle at rel L2 1e-4."""
     rng = np.random.default_rng(6)
-    L = 64 * 40
-    x, w, b = _r(rng, 1, 1, L), _r(rng, C_out, 1, k), _r(rng, C_out)
+    x, w, b = _r(rng, B, 1, L), _r(rng, C_out, 1, k), _r(rng, C_out)
     got = ops.conv1d(x, w, b, stride=s, padding=s // 2)
     assert rel_l2(got, nn.conv1d(x, w, b, stride=s, padding=s // 2)) < TOL
 
