@@ -54,7 +54,7 @@ struct AttnLds {
   static constexpr int V = AWAVES * ROWS * VSTRIDE;    // per-wave V tiles
   static constexpr int MERGE = (AWAVES - 1) * (DT * 16 * 64 + 2 * 32);
   static constexpr int R = 32 * 32;                    // R^T[r][t]
-  static constexpr int PB = AWAVES * 32 * 32;          // per-wave band probabilities [r][t]
+  static constexpr int PB = AWAVES * 33 * 32;          // per-wave band probabilities [r][t] + a junk row
   static constexpr int VM = V > MERGE ? V : MERGE;
   static constexpr int TOTAL = Q + VM + R + PB;
 };
@@ -82,8 +82,11 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   const int l32 = lane & 31;
   const long long CP = (long long)H * D * P;
   const float* qb = qkv + (long long)b * 3 * CP + (long long)h * D * P;
-  const float* kb = qb + CP;
-  const float* vb = qb + 2 * CP;
+  // one buffer resource per operand block ([D][P] each); masked lanes read 0
+  const unsigned blk = 4u * (unsigned)(D * P);
+  const __amdgpu_buffer_rsrc_t qrs = uniform_rsrc(qb, blk);
+  const __amdgpu_buffer_rsrc_t krs = uniform_rsrc(qb + CP, blk);
+  const __amdgpu_buffer_rsrc_t vrs = uniform_rsrc(qb + 2 * CP, blk);
   const int nb = emb_k != nullptr ? 2 * window + 1 : 0;  // no band: plain attention
   const int t = t0 + l32;
   const float sq = sqrtf((float)D);
@@ -91,20 +94,25 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   // stage qs[d][t] = q[d][t0 + t] / sqrt(D)
   for (int e = tid; e < Lds::Q; e += 256) {
     const int d = e >> 5, j = e & 31;
-    Qs[e] = (d < D && t0 + j < P) ? qb[(long long)d * P + t0 + j] / sq : 0.f;
+    const unsigned off = (d < D && t0 + j < P) ? 4u * (unsigned)(d * P + t0 + j) : kBufOut;
+    Qs[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(qrs, off, 0, 0)) / sq;
   }
-  float* Pb = PbAll + wave * 32 * 32;
-  for (int e = lane; e < 32 * 32; e += 64) Pb[e] = 0.f;
+  // band probabilities per wave: rows [0, nb) live, row 32 takes the masked
+  // lanes' (zero) updates so every lane can store unconditionally
+  float* Pb = PbAll + wave * 33 * 32;
+  for (int e = lane; e < 33 * 32; e += 64) Pb[e] = 0.f;
   __syncthreads();
   // R^T[r][t] = emb_k[r] . qs_t   (wave 0)
   if (wave == 0) {
+    const __amdgpu_buffer_rsrc_t ers = uniform_rsrc(emb_k, 4u * (unsigned)(nb * D));
     floatx16 racc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) racc[r] = 0.f;
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
       const int d = 2 * kk + half;
-      const float a = (l32 < nb && d < D) ? emb_k[l32 * D + d] : 0.f;
+      const unsigned off = (l32 < nb && d < D) ? 4u * (unsigned)(l32 * D + d) : kBufOut;
+      const float a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ers, off, 0, 0));
       racc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Qs[d * 32 + l32], racc, 0, 0, 0);
     }
 #pragma unroll
@@ -120,6 +128,7 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
     for (int r = 0; r < 16; ++r) O[dt][r] = 0.f;
   float m = -INFINITY;  // running max of query t (same in both half-waves)
   float l = 0.f;        // running sum over this half-wave's key rows
+  bool band_seen = false;  // wave-uniform: Pb holds probabilities to rescale
 
   const int ntile = (P + 31) / 32;
   const int per = (ntile + KS - 1) / KS;
@@ -127,20 +136,21 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   for (int kt = ks * per + wave; kt < kt_end; kt += AWAVES) {
     const int s0 = kt * 32;
     // all global loads of the tile first: K operands and the V tile
-    const bool key_ok = s0 + l32 < P;
+    // K operand kk and V staging element i read the same lane position:
+    // row 2 * kk + half (2 * i + half), key s0 + l32.  Rows at or past D fall
+    // outside the [D][P] block and read 0; a key past P takes an offset above
+    // every range (kBufOut + at most 63 row steps stays below 2^32, the
+    // launcher bounds P).
+    const unsigned base = s0 + l32 < P ? 4u * (unsigned)(half * P + s0 + l32) : kBufOut;
+    const unsigned rstep = 8u * (unsigned)P;
     float kreg[NKK];
 #pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) {
-      const int d = 2 * kk + half;
-      kreg[kk] = (d < D && key_ok) ? kb[(long long)d * P + s0 + l32] : 0.f;
-    }
+    for (int kk = 0; kk < NKK; ++kk)
+      kreg[kk] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(krs, base + kk * rstep, 0, 0));
     float vreg[DT * 16];
 #pragma unroll
-    for (int i = 0; i < DT * 16; ++i) {
-      const int e = lane + 64 * i;
-      const int d = e >> 5, j = e & 31;
-      vreg[i] = (d < D && s0 + j < P) ? vb[(long long)d * P + s0 + j] : 0.f;
-    }
+    for (int i = 0; i < DT * 16; ++i)
+      vreg[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vrs, base + i * rstep, 0, 0));
     // S^T[s][t] = sum_d k[d][s] qs[d][t]
     floatx16 S;
 #pragma unroll
@@ -153,18 +163,19 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
       const int e = lane + 64 * i;
       Vt[(e >> 5) * Lds::VSTRIDE + (e & 31)] = vreg[i];
     }
-    // band terms and key mask
-    const bool near = s0 <= t0 + 31 + window && s0 + 31 >= t0 - window;
+    // band terms (wave-uniform test) and key mask
+    const bool near = nb > 0 && s0 <= t0 + 31 + window && s0 + 31 >= t0 - window;
+    if (near) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int s = s0 + acc_row(r, half);
-      float v = S[r];
-      if (near) {
-        const int rr = s - t + window;
-        if (rr >= 0 && rr < nb) v = v + Rl[rr * 32 + l32];
+      for (int r = 0; r < 16; ++r) {
+        const int rr = s0 + acc_row(r, half) - t + window;
+        const bool in = (unsigned)rr < (unsigned)nb;
+        const float rv = Rl[(in ? rr : 0) * 32 + l32];
+        S[r] = in ? S[r] + rv : S[r];
       }
-      S[r] = s < P ? v : -INFINITY;
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) S[r] = s0 + acc_row(r, half) < P ? S[r] : -INFINITY;
     // online softmax statistics of query t
     float tm = S[0];
 #pragma unroll
@@ -185,13 +196,19 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) O[dt][r] *= alpha;
-    if (half == 0 && alpha != 1.f)
-      for (int rr = 0; rr < nb; ++rr) Pb[rr * 32 + l32] *= alpha;
+    if (band_seen) {
+      // the two half-waves rescale rows [0, 16) and [16, 32)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) Pb[(16 * half + i) * 32 + l32] *= alpha;
+    }
     if (near) {
+      band_seen = true;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int rr = s0 + acc_row(r, half) - t + window;
-        if (rr >= 0 && rr < nb) Pb[rr * 32 + l32] += S[r];
+        const bool in = (unsigned)rr < (unsigned)nb;
+        float* pe = Pb + (in ? rr : 32) * 32 + l32;
+        *pe = *pe + (in ? S[r] : 0.f);
       }
     }
     // O^T[d][t] += sum_s V[d][s] P^T[s][t]
@@ -205,14 +222,18 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   }
 
   // band contribution: O^T[d][t] += sum_r emb_v[r][d] Pb[r][t]
-  for (int kk = 0; kk < (nb + 1) / 2; ++kk) {
-    const int rr = 2 * kk + half;
-    const float bval = rr < nb ? Pb[rr * 32 + l32] : 0.f;
+  if (band_seen) {
+    const __amdgpu_buffer_rsrc_t ers = uniform_rsrc(emb_v, 4u * (unsigned)(nb * D));
+    for (int kk = 0; kk < (nb + 1) / 2; ++kk) {
+      const int rr = 2 * kk + half;
+      const float bval = Pb[rr * 32 + l32];  // rows in [nb, 32) stay zero
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int d = dt * 32 + l32;
-      const float a = (rr < nb && d < D) ? emb_v[rr * D + d] : 0.f;
-      O[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bval, O[dt], 0, 0, 0);
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = dt * 32 + l32;
+        const unsigned off = (rr < nb && d < D) ? 4u * (unsigned)(rr * D + d) : kBufOut;
+        const float a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ers, off, 0, 0));
+        O[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bval, O[dt], 0, 0, 0);
+      }
     }
   }
   l = l + __shfl_xor(l, 32);
@@ -343,6 +364,10 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
   RVC_CHECK(window >= 0 && window <= kMaxWindow, "relpos_attention: window must be in [0,15]");
   RVC_CHECK((emb_k == nullptr) == (emb_v == nullptr), "relpos_attention: emb_k and emb_v go together");
   RVC_CHECK(P >= 1 && B >= 1 && H >= 1, "relpos_attention: invalid shape");
+  // 32-bit buffer offsets: one [D][P] operand block, and the masked-key
+  // offset plus 63 row steps of 2P floats, stay below 2^31 / 2^32
+  RVC_CHECK((long long)D * P * 4 < (1LL << 31) && 63LL * 8 * P < (1LL << 31),
+            "relpos_attention: sequence too long for 32-bit offsets");
   const int KS = relpos_attention_splits(B, H, P);
   RVC_CHECK(KS == 1 || scratch != nullptr, "relpos_attention: scratch buffer required");
   const int dt = (D + 31) / 32;

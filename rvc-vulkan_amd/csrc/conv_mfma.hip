@@ -52,18 +52,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
-// A buffer resource from values the whole wave shares.  readfirstlane keeps
-// the descriptor in scalar registers even where the compiler placed one of
-// its inputs in a vector register (a descriptor in vector registers turns
-// every load through it into a waterfall loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, unsigned range) {
-  const unsigned long long v = reinterpret_cast<unsigned long long>(base);
-  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
-  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
-  void* p = reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)__builtin_amdgcn_readfirstlane(range), 0x00020000);
-}
-
 __device__ __forceinline__ float apply_act(float v, int act, float slope) {
   if (act == ACT_LEAKY) return v >= 0.f ? v : v * slope;
   if (act == ACT_TANH) return tanhf(v);

@@ -45,6 +45,21 @@ void check_launch(const char* what);
 // combine step of the epilogue.
 enum Act : int { ACT_NONE = 0, ACT_LEAKY = 1, ACT_TANH = 2, ACT_RELU = 3, ACT_GELU = 4, ACT_SIGMOID = 5 };
 
+// A raw buffer resource (32-bit offsets, out-of-range reads give 0 and
+// out-of-range writes are dropped) from values the whole wave shares.
+// readfirstlane keeps the descriptor in scalar registers even where the
+// compiler placed one of its inputs in a vector register (a descriptor in
+// vector registers turns every load through it into a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base, unsigned range) {
+  const unsigned long long v = reinterpret_cast<unsigned long long>(base);
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+  void* p = reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)__builtin_amdgcn_readfirstlane(range), 0x00020000);
+}
+// the offset a masked lane passes: above every range these kernels build
+constexpr unsigned kBufOut = 0x80000000u;
+
 // logistic function in the two-branch form of runtime/nn.py:520-523
 __device__ inline float sigmoid_as(float x) {
   if (x >= 0.f) return 1.0f / (1.0f + expf(-x));
