@@ -708,7 +708,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
 // tid / BN + RS * k.  Every global operand is loaded (buffer loads, rows and
 // columns out of range masked to the out-of-range offset) before the first
 // use.  Plain: out = combine(act(v + bias (+ bias2) (+ residual))), the
-// split-K reduce's order.  WaveNet gate (gate = true): tile rows [0, 16) are
+// split-K reduce's order (combine COMB_SUB, out = out - that, only here).  WaveNet gate (gate = true): tile rows [0, 16) are
 // channels cb + r, rows [16, 32) channels H + cb + r - 16, and
 // out[c] = tanh(v_c + g_c) * sigmoid(v_{H+c} + g_{H+c}) for the 16 channels
 // (v including the bias), g per batch item.
@@ -807,6 +807,8 @@ __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const C
       t = ov[k] + t;
     } else if (G.combine == COMB_ADD_DIV) {
       t = (ov[k] + t) / a.div;
+    } else if (G.combine == COMB_SUB) {
+      t = ov[k] - t;
     }
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, t), ors, oo[k], 0, 0);
   }
@@ -1222,8 +1224,17 @@ struct SplitPlan {
 // The small 1x1 GEMM path: every group a plain 1x1 conv (no stride, offset or
 // output interleave), at most 256 input channels (the whole reduction fits
 // LDS), a few thousand columns, no reduce post-op.
+// 32-bit buffer offsets of the small-conv kernels: x, the weights, out and
+// the residual each within 2 GiB of their batch item; grid z in range.
+bool small_offsets_ok(const ConvLaunch& a) {
+  const long long n_out = max_n_out(a);
+  return (long long)a.n_groups * a.B <= 65535 && 4LL * ((a.C_in - 1) * a.xc + a.L_in) < (1LL << 31) &&
+         4LL * a.g[0].K * a.C_in * a.w_ld < (1LL << 31) && 4LL * ((a.C_out - 1) * a.oc + n_out) < (1LL << 31) &&
+         4LL * ((a.C_out - 1) * a.rc + n_out) < (1LL << 31);
+}
+
 bool small_gemm_ok(const ConvLaunch& a) {
-  if (a.C_in > 256 || a.C_in % 8 != 0 || a.post != POST_NONE) return false;
+  if (a.C_in > 256 || a.C_in % 8 != 0 || a.post != POST_NONE || !small_offsets_ok(a)) return false;
   for (int g = 0; g < a.n_groups; ++g) {
     const ConvGroup& G = a.g[g];
     if (G.K != 1 || G.in_step > 1 || G.in_off != 0 || G.out_step != 1 || G.out_off != 0 || G.n_out > 8192 ||
@@ -1241,6 +1252,7 @@ bool small_gemm_ok(const ConvLaunch& a) {
 bool small_conv_ok(const ConvLaunch& a) {
   const int K = a.g[0].K;
   if (K == 1 ? (a.C_in % 128 != 0 || a.C_in > 4096) : (a.C_in % 64 != 0 || a.C_in > 1024)) return false;
+  if (!small_offsets_ok(a)) return false;
   if (a.post == POST_WN_GATE) {
     if (a.n_groups != 1 || a.post_H % 16 != 0 || a.C_out != 2 * a.post_H) return false;
   } else if (a.post != POST_NONE) {
@@ -1280,11 +1292,6 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   const int nco = gate ? a.post_H / 16 : (a.C_out + 31) / 32;
   const long long z = (long long)a.n_groups * a.B;
   const int K = a.g[0].K;
-  // 32-bit buffer offsets: x, the weights, out and the residual within 2 GiB
-  if (z > 65535 || 4LL * ((a.C_in - 1) * a.xc + a.L_in) >= (1LL << 31) ||
-      4LL * K * a.C_in * a.w_ld >= (1LL << 31) || 4LL * ((a.C_out - 1) * a.oc + n_out) >= (1LL << 31) ||
-      4LL * ((a.C_out - 1) * a.rc + n_out) >= (1LL << 31))
-    return false;
   // 64-column tiles while they give ~256 workgroups, else 32 (the reduction
   // order does not depend on the tile width or the batch)
   const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 192;
@@ -1312,10 +1319,6 @@ bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
   for (int g = 0; g < a.n_groups; ++g) n_out = std::max(n_out, a.g[g].n_out);
   const int nco = (a.C_out + 31) / 32;
   const long long z = (long long)a.n_groups * a.B;
-  // 32-bit buffer offsets: x, out and the residual each within 2 GiB of their batch item
-  if (z > 65535 || 4LL * ((a.C_in - 1) * a.xc + a.L_in) >= (1LL << 31) ||
-      4LL * ((a.C_out - 1) * a.oc + n_out) >= (1LL << 31) || 4LL * ((a.C_out - 1) * a.rc + n_out) >= (1LL << 31))
-    return false;
   const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 192;
   const int BN = wide ? 64 : 32;
   const size_t n_it = (size_t)a.C_in / (256 / BN);  // staging passes, rounded up to the batch of 16
@@ -1393,6 +1396,10 @@ void launch_splitk_reduce(const ConvLaunch& a, hipStream_t s) {
   check_launch("splitk_reduce");
 }
 
+bool conv1d_mfma_small_path(const ConvLaunch& a) {
+  return a.g[0].in_step <= 1 && (small_gemm_ok(a) || small_conv_ok(a));
+}
+
 bool conv1d_mfma_fuses_gate(const ConvLaunch& a) {
   ConvLaunch t = a;
   t.post = POST_WN_GATE;
@@ -1426,6 +1433,8 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   if (max_n_out(a) == 0) return;
   if (step == 1 && small_gemm_ok(a) && launch_small_gemm(a, s)) return;
   if (step == 1 && small_conv_ok(a) && launch_small_conv(a, s)) return;
+  for (int g = 0; g < a.n_groups; ++g)
+    RVC_CHECK(a.g[g].combine != COMB_SUB, "conv1d_mfma: the subtracting combine runs on the small-conv kernels only");
   // Tile choice: widest co tile that divides C_out while the grid still
   // gives every CU work (256 CUs); few output columns -> split-K waves.
   // The 128 x 128 tile (two resident workgroups per CU) also needs about two

@@ -88,6 +88,7 @@ enum Combine : int {
   COMB_STORE = 0,    // out = v
   COMB_ADD = 1,      // out = out + v
   COMB_ADD_DIV = 2,  // out = (out + v) / div
+  COMB_SUB = 3,      // out = out - v (the small-conv kernels only: conv1d_mfma_small_path)
 };
 
 // MFMA fast path bounds: taps per conv and the input halo (K-1)*dil.
@@ -160,6 +161,9 @@ size_t conv1d_mfma_split_floats(const ConvLaunch& a);
 // path that applies the gate (split-K reduce or the small-conv kernel); the
 // caller adds a separate gate launch otherwise.
 bool conv1d_mfma_fuses_gate(const ConvLaunch& a);
+// Whether the launch runs on the small-conv (whole-reduction) kernels, the
+// only ones that take COMB_SUB.
+bool conv1d_mfma_small_path(const ConvLaunch& a);
 void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s);
 // out = combine(act(sum of the split-K partials + bias ...)) for a launch
 // with a.ksplit > 1 (shared by the fp32 and bf16 kernels)

@@ -52,12 +52,18 @@ struct Synth : SessionBase {
   float *proj_w = nullptr, *proj_b = nullptr;
   uint16_t *emb_phone16 = nullptr, *proj16 = nullptr;
   int precision = 0;
+  // A flow entered with its channels reversed relative to the reference's
+  // (see flow()) reads the pre conv's half with the weight's input channels
+  // reversed, and subtracts the post conv's rows in reverse order.
   struct FlowL {
-    float *pre_w, *pre_b, *post_w, *post_b, *cond_w, *cond_b;
+    bool rev;
+    float *pre_w, *pre_b, *post_w, *post_b;
     float *in_w[kWnLayers], *in_b[kWnLayers], *rs_w[kWnLayers], *rs_b[kWnLayers];
     int rs_out[kWnLayers];
   };
   std::vector<FlowL> flows;
+  // every flow's cond_layer stacked, [n_flows * 2H * kWnLayers][gin]
+  float *flow_cond_w = nullptr, *flow_cond_b = nullptr;
   float *dpre_w = nullptr, *dpre_b = nullptr, *dcond_w = nullptr, *dcond_b = nullptr, *dpost_w = nullptr;
   float w_lin = 0.f, b_lin = 0.f;
   struct StageW {
@@ -245,17 +251,37 @@ struct Synth : SessionBase {
     proj_b = upload_vec("enc_p.proj.bias", 2 * H);
 
     // ---- flow ----
+    const long long GW = 2LL * H * kWnLayers;  // cond rows per flow
+    std::vector<float> cond_w, cond_b;
     for (int fi = 0; fi < n_flows; ++fi) {
       const std::string b = "flow.flows." + std::to_string(2 * fi);
       FlowL L{};
-      L.pre_w = upload_conv(b + ".pre", H, half, 1, false);
+      // flow() runs the flows from the last to the first, the channel order
+      // reversed (relative to the reference's) on the 1st, 3rd, ... of them
+      L.rev = ((n_flows - fi) & 1) != 0;
+      std::vector<float> pw = conv_host(b + ".pre", H, half, 1, false);
+      std::vector<float> qw = conv_host(b + ".post", half, H, 1, false);
+      std::vector<float> qb = W(b + ".post.bias").data;
+      RVC_CHECK((long long)qb.size() == half, "weight " + b + ".post.bias must hold " + std::to_string(half) + " values");
+      if (L.rev) {
+        for (long long o = 0; o < H; ++o) std::reverse(pw.begin() + o * half, pw.begin() + (o + 1) * half);
+        std::vector<float> rq(qw.size());
+        for (long long o = 0; o < half; ++o)
+          std::copy(qw.begin() + (half - 1 - o) * H, qw.begin() + (half - o) * H, rq.begin() + o * H);
+        qw.swap(rq);
+        std::reverse(qb.begin(), qb.end());
+      }
+      L.pre_w = upload(pack(pw, H, half, 1));
       L.pre_b = upload_vec(b + ".pre.bias", H);
-      L.post_w = upload_conv(b + ".post", half, H, 1, false);
-      L.post_b = upload_vec(b + ".post.bias", half);
+      L.post_w = upload(pack(qw, half, H, 1));
+      L.post_b = upload(qb);
       const HostT& cv = W(b + ".enc.cond_layer.weight_v");
-      check_shape(b + ".enc.cond_layer.weight_v", cv.shape, {2 * H * kWnLayers, gin, 1});
-      L.cond_w = upload(deweight(b + ".enc.cond_layer"));
-      L.cond_b = upload_vec(b + ".enc.cond_layer.bias", 2 * H * kWnLayers);
+      check_shape(b + ".enc.cond_layer.weight_v", cv.shape, {GW, gin, 1});
+      const std::vector<float> cw = deweight(b + ".enc.cond_layer");
+      cond_w.insert(cond_w.end(), cw.begin(), cw.end());
+      const HostT& cb = W(b + ".enc.cond_layer.bias");
+      RVC_CHECK((long long)cb.data.size() == GW, "weight " + b + ".enc.cond_layer.bias has the wrong size");
+      cond_b.insert(cond_b.end(), cb.data.begin(), cb.data.end());
       for (int i = 0; i < kWnLayers; ++i) {
         const std::string il = b + ".enc.in_layers." + std::to_string(i);
         L.in_w[i] = upload_conv(il, 2 * H, H, kWnKernel, true);
@@ -267,6 +293,8 @@ struct Synth : SessionBase {
       }
       flows.push_back(L);
     }
+    flow_cond_w = upload(cond_w);
+    flow_cond_b = upload(cond_b);
 
     // ---- dec ----
     dpre_w = upload_conv("dec.conv_pre", U, H, 7, false);
@@ -415,25 +443,36 @@ struct Synth : SessionBase {
   }
 
   // flow.reverse of src [B][H][P] (batch stride H*P): Flip, RC(6), Flip,
-  // RC(4), ... RC(0).  Returns z [B][H][P] in a workspace buffer.
+  // RC(4), ... RC(0) (runtime/models/vits.py, ResidualCouplingBlock reverse).
+  // The flips move no data: X holds the reference's tensor with its channel
+  // order reversed after an odd number of flips, and such a flow reads its
+  // pre conv's half from the top of X with the weight's input channels
+  // reversed and subtracts the post conv (rows reversed) from the bottom half
+  // (FlowL::rev, set up at finalize).  Each flow's x1 - m is the post conv's
+  // subtracting combine where the small-conv kernels run (up to 8192 frames),
+  // a separate elementwise launch otherwise; every flow's cond_layer(g) is one
+  // stacked gemv up front.  Returns z [B][H][P] in a workspace buffer.
   const float* flow(const float* src, int B, int P, const float* g) {
     hipStream_t s = eng->stream;
     const long long HP = (long long)H * P;
-    float* fz[2] = {buf("fz0", (size_t)B * HP), buf("fz1", (size_t)B * HP)};
+    const long long GW = 2LL * H * kWnLayers;
+    float* X = buf("fz0", (size_t)B * HP);
     float* h = buf("fh", (size_t)B * HP);
-    float* gv = buf("fgv", (size_t)B * 2 * H * kWnLayers);
+    float* gv = buf("fgv", (size_t)B * n_flows * GW);
     float* skip = buf("fskip", (size_t)B * HP);
     float* xi = buf("fxi", (size_t)B * 2 * HP);
     float* acts = buf("facts", (size_t)B * HP);
-    float* m = buf("fm", (size_t)B * half * P);
-    int k = 0;
+    run("flow.glue", 0.0, 8.0 * B * HP,
+        [&] { RVC_HIP(hipMemcpyAsync(X, src, sizeof(float) * B * HP, hipMemcpyDeviceToDevice, s)); });
+    run("flow.glue", 2.0 * B * gin * n_flows * GW, 4.0 * (B * gin + (double)(gin + 1 + B) * n_flows * GW),
+        [&] { launch_gemv(flow_cond_w, flow_cond_b, g, gin, gv, n_flows * GW, B, (int)(n_flows * GW), gin, s); });
     for (int fi = n_flows - 1; fi >= 0; --fi) {
       const FlowL& L = flows[fi];
-      float* dst = fz[k];
-      run("flow.glue", 0.0, 8.0 * B * HP, [&] { launch_flip_channels(src, dst, B, H, P, s); });
-      conv("flow.pre", c1x1(dst, HP, L.pre_w, L.pre_b, h, B, half, H, P));
-      run("flow.glue", 2.0 * B * gin * 2.0 * H * kWnLayers, 4.0 * (B * gin + (double)(gin + 1 + B) * 2 * H * kWnLayers),
-          [&] { launch_gemv(L.cond_w, L.cond_b, g, gin, gv, (long long)2 * H * kWnLayers, B, 2 * H * kWnLayers, gin, s); });
+      const long long lo = 0, hi = (long long)half * P;  // channel offsets of X's halves
+      const float* x0 = X + (L.rev ? hi : lo);
+      float* x1 = X + (L.rev ? lo : hi);
+      const float* gf = gv + (long long)fi * GW;
+      conv("flow.pre", c1x1(x0, HP, L.pre_w, L.pre_b, h, B, half, H, P));
       for (int i = 0; i < kWnLayers; ++i) {
         // in-layer conv + gate: fused into the small-conv kernel's epilogue
         // or the split-K reduce when the conv takes one of those paths (it
@@ -442,8 +481,8 @@ struct Synth : SessionBase {
                                    (kWnKernel - 1) / 2);
         if (conv1d_mfma_fuses_gate(ci)) {
           ci.post = POST_WN_GATE;
-          ci.post_g = gv + (long long)i * 2 * H;
-          ci.post_gb = (long long)2 * H * kWnLayers;
+          ci.post_g = gf + (long long)i * 2 * H;
+          ci.post_gb = n_flows * GW;
           ci.post_H = H;
           ci.g[0].out = acts;
           ci.ob = HP;
@@ -452,7 +491,7 @@ struct Synth : SessionBase {
         } else {
           conv("flow.in", ci);
           run("flow.glue", 0.0, 12.0 * B * HP, [&] {
-            launch_wn_gate(xi, 2 * HP, gv + (long long)i * 2 * H, (long long)2 * H * kWnLayers, acts, B, H, P, s);
+            launch_wn_gate(xi, 2 * HP, gf + (long long)i * 2 * H, n_flows * GW, acts, B, H, P, s);
           });
         }
         // res/skip conv as one launch of two output groups over the same
@@ -481,14 +520,28 @@ struct Synth : SessionBase {
         }
         conv("flow.rs", cr);
       }
-      conv("flow.post", c1x1(skip, HP, L.post_w, L.post_b, m, B, H, half, P));
-      run("flow.glue", (double)B * half * P, 12.0 * B * half * P,
-          [&] { launch_sub_inplace_strided(dst + (long long)half * P, HP, m, (long long)half * P, B, half, P, s); });
-      src = dst;
-      z_name = k == 0 ? "fz0" : "fz1";
-      k ^= 1;
+      // x1 = x1 - (post(skip) + b), into X's other half (batch stride HP)
+      ConvLaunch cp = c1x1(skip, HP, L.post_w, L.post_b, x1, B, H, half, P);
+      cp.ob = HP;
+      cp.g[0].combine = COMB_SUB;
+      if (conv1d_mfma_small_path(cp)) {
+        conv("flow.post", cp);
+      } else {
+        float* m = buf("fm", (size_t)B * half * P);
+        conv("flow.post", c1x1(skip, HP, L.post_w, L.post_b, m, B, H, half, P));
+        run("flow.glue", (double)B * half * P, 12.0 * B * half * P,
+            [&] { launch_sub_inplace_strided(x1, HP, m, (long long)half * P, B, half, P, s); });
+      }
     }
-    return src;
+    z_name = "fz0";
+    if (flows.size() % 2 != 0) {
+      // an odd number of flips leaves X reversed: one physical flip
+      float* Z = buf("fz1", (size_t)B * HP);
+      run("flow.glue", 0.0, 8.0 * B * HP, [&] { launch_flip_channels(X, Z, B, H, P, s); });
+      z_name = "fz1";
+      return Z;
+    }
+    return X;
   }
 
   // enc_p + flow over all P frames (infer_controlled's z)
