@@ -31,6 +31,22 @@ bytes (``bench.py --calibrate-copy MIB``):
 It prints a table per launch shape and one machine-readable line for the
 ResBlock family, ``resblock_traffic_bytes_per_launch: N``, which ``bench.py``
 reads from the committed summary.
+
+With ``--sq`` it turns two ``--pmc`` databases of SQ counters into MFMA
+utilisation and instruction mix per launch shape:
+
+    pass A: SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY
+            SQ_ACTIVE_INST_ANY SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA
+    pass B: SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_VALU
+            SQ_INSTS_SALU SQ_INSTS_VMEM_RD (optional)
+
+    python -m rvc_hip.profsum --sq pass_a.db [pass_b.db]
+
+MFMA busy is SQ_VALU_MFMA_BUSY_CYCLES (summed over every SIMD) divided by
+the SIMD-cycles of the dispatch: 1024 SIMDs x duration x clock, once at the
+2.4 GHz peak engine clock (the basis of the published 157.3 TFLOP/s) and once
+at the clock the shader engines actually ran (SQ_BUSY_CYCLES / 32 engines /
+duration).
 """
 
 from __future__ import annotations
@@ -117,6 +133,70 @@ def traffic(fetch_db: str, write_db: str, copy_fetch: str, copy_write: str, mib:
     return 0
 
 
+N_SIMD, N_SE, PEAK_GHZ = 1024, 32, 2.4
+
+
+def _sq(db: str):
+    """{(kernel, grid): {counter: mean per dispatch}}, dispatch counts and
+    mean durations (ns), from the database's per-dispatch counter view."""
+    con = sqlite3.connect(db)
+    q = ("select dispatch_id, kernel_name, grid_size_x, grid_size_y, grid_size_z, workgroup_size_x, "
+         "counter_name, value, duration from counters_collection")
+    per, key = {}, {}
+    for did, name, gx, gy, gz, wx, cn, v, d in con.execute(q):
+        key[did] = ((_short(name), (gx // max(wx, 1), gy, gz)), d)
+        per.setdefault(did, {})[cn] = v
+    means, counts, dur = {}, {}, {}
+    for did, cs in per.items():
+        k, d = key[did]
+        counts[k] = counts.get(k, 0) + 1
+        dur[k] = dur.get(k, 0.0) + d
+        m = means.setdefault(k, {})
+        for cn, v in cs.items():
+            m[cn] = m.get(cn, 0.0) + v
+    for k in means:
+        for cn in means[k]:
+            means[k][cn] /= counts[k]
+        dur[k] /= counts[k]
+    return means, counts, dur
+
+
+def sq_summary(db_a: str, db_b: str = None) -> int:
+    a, n, dur = _sq(db_a)
+    b = _sq(db_b)[0] if db_b else {}
+    print("| kernel | grid | dispatches | us | clock GHz | MFMA busy at 2.4 GHz | MFMA busy at run clock | "
+          "wait / waitcnt | wait / issue | VALU per MFMA | SALU per MFMA | LDS per MFMA | bank-conflict cycles |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    fam = [0.0, 0.0, 0.0]  # busy cycles, SIMD-cycles at 2.4 GHz, at run clock
+    for k in sorted(a, key=lambda k: -dur.get(k, 0) * n[k]):
+        c = a[k]
+        if "SQ_VALU_MFMA_BUSY_CYCLES" not in c or k not in dur:
+            continue
+        d = dur[k] * 1e-9
+        busy = c["SQ_VALU_MFMA_BUSY_CYCLES"]
+        clk = c.get("SQ_BUSY_CYCLES", 0.0) / N_SE / d / 1e9 if d > 0 else 0.0
+        at_peak = busy / (N_SIMD * d * PEAK_GHZ * 1e9) if d > 0 else 0.0
+        at_run = busy / (N_SIMD * d * clk * 1e9) if clk > 0 else 0.0
+        w = max(c.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        cb = b.get(k, {})
+        mix = (f"{cb['SQ_INSTS_VALU'] / mf:.2f} | {cb['SQ_INSTS_SALU'] / mf:.2f} | {cb['SQ_INSTS_LDS'] / mf:.2f} | "
+               f"{cb['SQ_LDS_BANK_CONFLICT'] / max(cb['SQ_LDS_IDX_ACTIVE'], 1.0):.2f}"
+               if mf > 0 and {"SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT",
+                              "SQ_LDS_IDX_ACTIVE"} <= set(cb) else "- | - | - | -")
+        print(f"| {k[0]} | {k[1]} | {n[k]} | {dur[k] / 1e3:.1f} | {clk:.2f} | {at_peak:.3f} | {at_run:.3f} | "
+              f"{c.get('SQ_WAIT_ANY', 0.0) / w:.2f} | {c.get('SQ_WAIT_INST_ANY', 0.0) / w:.2f} | {mix} |")
+        if is_resblock(*k):
+            fam[0] += busy * n[k]
+            fam[1] += N_SIMD * d * PEAK_GHZ * 1e9 * n[k]
+            fam[2] += N_SIMD * d * clk * 1e9 * n[k]
+    if fam[1] > 0:
+        print(f"\nResBlock family (persistent FAM 1, or one-shot grid z = 3 and >= 64 wide):")
+        print(f"resblock_mfma_busy_at_peak_clock: {fam[0] / fam[1]:.3f}")
+        print(f"resblock_mfma_busy_at_run_clock: {fam[0] / fam[2]:.3f}")
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("db")
@@ -128,7 +208,10 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=0, help="timed steps in the run (per-step figures)")
     ap.add_argument("--top", type=int, default=30)
     ap.add_argument("--pmc", action="store_true")
+    ap.add_argument("--sq", action="store_true", help="SQ-counter MFMA utilisation (db = pass A, db2 = pass B)")
     args = ap.parse_args(argv)
+    if args.sq:
+        return sq_summary(args.db, args.db2)
     if args.traffic:
         if not (args.db2 and args.copy_fetch and args.copy_write):
             ap.error("--traffic needs FETCH and WRITE databases and --copy-fetch / --copy-write")
