@@ -1292,9 +1292,12 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   const int nco = gate ? a.post_H / 16 : (a.C_out + 31) / 32;
   const long long z = (long long)a.n_groups * a.B;
   const int K = a.g[0].K;
-  // 64-column tiles while they give ~256 workgroups, else 32 (the reduction
-  // order does not depend on the tile width or the batch)
-  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 192;
+  // 64-column tiles when they give at least 320 workgroups, else 32: below
+  // that, twice the workgroups (two waves per SIMD on more CUs) beat the wider
+  // tile's operand reuse (config 2: flow 0.375 -> 0.360 ms, enc_p 0.725 ->
+  // 0.709 ms against a threshold of 192).  The reduction order does not
+  // depend on the tile width or the batch.
+  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 320;
   const int BN = wide ? 64 : 32;
   // 128-channel chunks for the long 3-tap reductions (enc_p's FFN output
   // conv, C_in = 768): half the chunk round trips
@@ -1319,7 +1322,7 @@ bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
   for (int g = 0; g < a.n_groups; ++g) n_out = std::max(n_out, a.g[g].n_out);
   const int nco = (a.C_out + 31) / 32;
   const long long z = (long long)a.n_groups * a.B;
-  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 192;
+  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 320;  // as in launch_small_conv
   const int BN = wide ? 64 : 32;
   const size_t n_it = (size_t)a.C_in / (256 / BN);  // staging passes, rounded up to the batch of 16
   const size_t lds = sizeof(float) * (256 * 32 + (n_it + 15) / 16 * 16 * 256);
