@@ -703,21 +703,21 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
 // (((q0 + q1) + q2) + q3) -- one launch and no partial-sum tensor, where the
 // split-K path writes and re-reads every split's partial tile.
 
-// The shared epilogue: each wave stores its 32 x BN accumulators to red
-// [wave][n][r][lane], then thread tid forms column i0 + tid % BN of tile rows
-// tid / BN + RS * k.  Every global operand is loaded (buffer loads, rows and
+// The shared epilogue: each of the NW waves stores its 32 x BN accumulators
+// to red [wave][n][r][lane], the partial tiles are added in wave order, and
+// thread tid forms column i0 + tid % BN of tile rows tid / BN + RS * k.  Every global operand is loaded (buffer loads, rows and
 // columns out of range masked to the out-of-range offset) before the first
 // use.  Plain: out = combine(act(v + bias (+ bias2) (+ residual))), the
 // split-K reduce's order (combine COMB_SUB, out = out - that, only here).  WaveNet gate (gate = true): tile rows [0, 16) are
 // channels cb + r, rows [16, 32) channels H + cb + r - 16, and
 // out[c] = tanh(v_c + g_c) * sigmoid(v_{H+c} + g_{H+c}) for the 16 channels
 // (v including the bias), g per batch item.
-template <int BN>
+template <int BN, int NW = 4>
 __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const ConvGroup& G, int b, int i0, int co0,
                                                     bool gate, const floatx16 (&acc)[BN / 32], float* red) {
   constexpr int TN = BN / 32;
-  constexpr int RS = 256 / BN;
-  constexpr int KO = 32 * BN / 256;
+  constexpr int RS = 64 * NW / BN;
+  constexpr int KO = 32 * BN / (64 * NW);
   constexpr unsigned kOut = 0x80000000u;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -742,10 +742,10 @@ __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const C
     const int row = tid / BN + k * RS;
     const int r = (row >> 3) * 4 + (row & 3);
     const int ln = c32 + 32 * ((row >> 2) & 1);
-    float t = red[((0 * TN + n) * 16 + r) * 64 + ln];
-    t = t + red[((1 * TN + n) * 16 + r) * 64 + ln];
-    t = t + red[((2 * TN + n) * 16 + r) * 64 + ln];
-    v[k] = t + red[((3 * TN + n) * 16 + r) * 64 + ln];
+    float t = red[(n * 16 + r) * 64 + ln];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t = t + red[((w * TN + n) * 16 + r) * 64 + ln];
+    v[k] = t;
     const int co = gate ? (row < 16 ? co0 + row : H + co0 + row - 16) : co0 + row;
     const bool ok = icol && co < a.C_out;
     bo[k] = ok ? 4u * (unsigned)co : kOut;
@@ -919,20 +919,22 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
 // reduction streams through LDS in chunks of CHK input channels with all K
 // taps -- W[0:K][c0:c0+CHK][32 rows] and x[c0:c0+CHK][i0+in_off : +BN+K-1] --
 // the next chunk's loads in flight (registers) while the current one is
-// multiplied.  Wave w takes channels [w*CHK/4, (w+1)*CHK/4) of every chunk,
-// two per MFMA (k = lane / 32), the K taps innermost.  POST_WN_GATE launches
+// multiplied.  Wave w of NW takes channels [w*CHK/NW, (w+1)*CHK/NW) of every
+// chunk, two per MFMA (k = lane / 32), the K taps innermost.  POST_WN_GATE launches
 // map tile rows to channel pairs (16 tanh channels and their sigmoid
 // partners, cb = blockIdx.y * 16).
-template <int BN, int K, int CHK>
-__global__ __launch_bounds__(256) void conv_small_kernel(ConvLaunch a) {
+template <int BN, int K, int CHK, int NW>
+__global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
+  constexpr int NT = 64 * NW;
   constexpr int TN = BN / 32;
   constexpr int XW = BN + K - 1;             // staged input columns per channel
-  constexpr int WF4 = K * CHK / 32;          // float4 weight loads per thread per chunk
-  constexpr int XE = (CHK * XW + 255) / 256; // input loads per thread per chunk
+  static_assert((K * CHK * 8) % NT == 0 && CHK % (2 * NW) == 0, "whole float4 rows and MFMA steps per wave");
+  constexpr int WF4 = K * CHK * 8 / NT;      // float4 weight loads per thread per chunk
+  constexpr int XE = (CHK * XW + NT - 1) / NT; // input loads per thread per chunk
   constexpr unsigned kOut = 0x80000000u;
   extern __shared__ float smem[];
   float* ws = smem;                // [K][CHK][32]
-  float* xs = smem + K * CHK * 32; // [XE * 256] (CHK rows of XW, tail unused)
+  float* xs = smem + K * CHK * 32; // [XE * NT] (CHK rows of XW, tail unused)
   const int b = blockIdx.z % a.B;
   const int gi = blockIdx.z / a.B;
   const ConvGroup& G = a.g[gi];
@@ -957,7 +959,7 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvLaunch a) {
   unsigned wo[WF4];
 #pragma unroll
   for (int j = 0; j < WF4; ++j) {
-    const int f = j * 256 + tid;  // float4 index in [K][CHK][8]
+    const int f = j * NT + tid;  // float4 index in [K][CHK][8]
     const int kc = f >> 3;
     const int k = kc / CHK, ci = kc - k * CHK;
     const int r4 = 4 * (f & 7);
@@ -967,7 +969,7 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvLaunch a) {
   unsigned xo[XE];
 #pragma unroll
   for (int j = 0; j < XE; ++j) {
-    const int e = j * 256 + tid;
+    const int e = j * NT + tid;
     const int ci = e / XW;
     const int t = i0 + G.in_off + (e - ci * XW);
     xo[j] = (e < CHK * XW && t >= 0 && t < a.L_in) ? 4u * (unsigned)(ci * (int)a.xc + t) : kOut;
@@ -991,18 +993,18 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvLaunch a) {
   for (int n = 0; n < TN; ++n)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
-  constexpr int Q = CHK / 4;
+  constexpr int Q = CHK / NW;
   const float* wl = ws + (wave * Q + half) * 32 + l32;
   const float* xl = xs + (wave * Q + half) * XW + l32;
   load(0);
   for (int c = 0; c < n_ch; ++c) {
 #pragma unroll
-    for (int j = 0; j < WF4; ++j) reinterpret_cast<float4*>(ws)[j * 256 + tid] = wv[j];
+    for (int j = 0; j < WF4; ++j) reinterpret_cast<float4*>(ws)[j * NT + tid] = wv[j];
 #pragma unroll
     for (int j = 0; j < XE; ++j) {
       float u = xv[j];
       if (leaky) u = u >= 0.f ? u : u * a.in_slope;
-      xs[j * 256 + tid] = u;
+      xs[j * NT + tid] = u;
     }
     __syncthreads();
     if (c + 1 < n_ch) load(c + 1);
@@ -1022,7 +1024,7 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvLaunch a) {
     }
     if (c + 1 < n_ch) __syncthreads();  // the next chunk's stores overwrite this one
   }
-  small_conv_epilogue<BN>(a, G, b, i0, co0, gate, acc, smem);
+  small_conv_epilogue<BN, NW>(a, G, b, i0, co0, gate, acc, smem);
 }
 
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
@@ -1268,21 +1270,23 @@ bool small_conv_ok(const ConvLaunch& a) {
   return n_blocks(a, 64, 128) < 384;
 }
 
-template <int BN, int K, int CHK>
+template <int BN, int K, int CHK, int NW>
 void launch_small_conv_cfg(const ConvLaunch& a, dim3 grid, hipStream_t s) {
-  constexpr int XE = (CHK * (BN + K - 1) + 255) / 256;
-  constexpr size_t lds = sizeof(float) * ((size_t)K * CHK * 32 + (size_t)XE * 256);
-  static_assert(lds >= sizeof(float) * 4 * (BN / 32) * 16 * 64, "the epilogue's reduction must fit the staging LDS");
+  constexpr int NT = 64 * NW;
+  constexpr int XE = (CHK * (BN + K - 1) + NT - 1) / NT;
+  constexpr size_t lds_stage = sizeof(float) * ((size_t)K * CHK * 32 + (size_t)XE * NT);
+  constexpr size_t lds_red = sizeof(float) * NW * (BN / 32) * 16 * 64;  // the epilogue's partial tiles
+  constexpr size_t lds = lds_stage > lds_red ? lds_stage : lds_red;
   static_assert(lds <= 160 * 1024, "staging LDS above the CU's 160 KiB");
   if (lds > 65536) {
     static bool attr = false;  // per instantiation
     if (!attr) {
-      RVC_HIP(hipFuncSetAttribute((const void*)conv_small_kernel<BN, K, CHK>,
+      RVC_HIP(hipFuncSetAttribute((const void*)conv_small_kernel<BN, K, CHK, NW>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
       attr = true;
     }
   }
-  hipLaunchKernelGGL((conv_small_kernel<BN, K, CHK>), grid, dim3(256), lds, s, a);
+  hipLaunchKernelGGL((conv_small_kernel<BN, K, CHK, NW>), grid, dim3(NT), lds, s, a);
 }
 
 bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
@@ -1303,15 +1307,20 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   // conv, C_in = 768): half the chunk round trips
   const int CHK = K == 3 && a.C_in % 128 == 0 && a.C_in >= 512 ? 128 : 64;
   const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
+  // Waves per workgroup: eight (each taking an eighth of every chunk's
+  // channels) for the K-tap convs, four for the wide 1x1 GEMMs.  Measured at
+  // config 2 against four waves: FFN output conv 24.6 -> 20.6 us, WaveNet
+  // in-layer 18.2 -> 16.7 us, FFN input conv 19.3 -> 17.8 us.  A function of
+  // the shape only, never of B: the wave count sets the summation order.
   if (K == 1) {
-    wide ? launch_small_conv_cfg<64, 1, 128>(a, grid, s) : launch_small_conv_cfg<32, 1, 128>(a, grid, s);
+    wide ? launch_small_conv_cfg<64, 1, 128, 4>(a, grid, s) : launch_small_conv_cfg<32, 1, 128, 4>(a, grid, s);
   } else if (K == 3) {
     if (CHK == 128)
-      wide ? launch_small_conv_cfg<64, 3, 128>(a, grid, s) : launch_small_conv_cfg<32, 3, 128>(a, grid, s);
+      wide ? launch_small_conv_cfg<64, 3, 128, 8>(a, grid, s) : launch_small_conv_cfg<32, 3, 128, 8>(a, grid, s);
     else
-      wide ? launch_small_conv_cfg<64, 3, 64>(a, grid, s) : launch_small_conv_cfg<32, 3, 64>(a, grid, s);
+      wide ? launch_small_conv_cfg<64, 3, 64, 8>(a, grid, s) : launch_small_conv_cfg<32, 3, 64, 8>(a, grid, s);
   } else {
-    wide ? launch_small_conv_cfg<64, 5, 64>(a, grid, s) : launch_small_conv_cfg<32, 5, 64>(a, grid, s);
+    wide ? launch_small_conv_cfg<64, 5, 64, 8>(a, grid, s) : launch_small_conv_cfg<32, 5, 64, 8>(a, grid, s);
   }
   check_launch("conv_small");
   return true;
