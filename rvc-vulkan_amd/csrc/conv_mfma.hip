@@ -915,7 +915,7 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
   small_conv_epilogue<BN>(a, G, b, i0, co0, false, acc, smem);
 }
 
-// K-tap convs (K = 3 or 5, dilation 1, stride 1), C_in % CHK == 0: the
+// K-tap convs (K = 3, 5 or 7, dilation 1, stride 1), C_in % CHK == 0: the
 // reduction streams through LDS in chunks of CHK input channels with all K
 // taps -- W[0:K][c0:c0+CHK][32 rows] and x[c0:c0+CHK][i0+in_off : +BN+K-1] --
 // the next chunk's loads in flight (registers) while the current one is
@@ -1246,8 +1246,8 @@ bool small_gemm_ok(const ConvLaunch& a) {
   return true;
 }
 
-// The chunked path: K = 3 or 5 at dilation 1 in every group (C_in a multiple
-// of 64 up to 1024), or 1x1 GEMMs too wide for the whole-reduction kernel
+// The chunked path: K = 3, 5 or 7 at dilation 1 in every group (C_in a
+// multiple of 64 up to 1024), or 1x1 GEMMs too wide for the whole-reduction kernel
 // (C_in a multiple of 128 up to 4096); stride 1, a few thousand columns and a
 // tile grid too small to fill the GPU (where the split-K path would run); the
 // reduce post-op POST_WN_GATE when C_out = 2 * post_H with post_H % 16 == 0.
@@ -1260,7 +1260,7 @@ bool small_conv_ok(const ConvLaunch& a) {
   } else if (a.post != POST_NONE) {
     return false;
   }
-  if (K != 1 && K != 3 && K != 5) return false;
+  if (K != 1 && K != 3 && K != 5 && K != 7) return false;
   for (int g = 0; g < a.n_groups; ++g) {
     const ConvGroup& G = a.g[g];
     if (G.K != K || G.dil != 1 || G.in_step > 1 || G.out_step != 1 || G.out_off != 0 || G.n_out > 8192 ||
@@ -1321,8 +1321,10 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
       wide ? launch_small_conv_cfg<64, 3, 128, 16>(a, grid, s) : launch_small_conv_cfg<32, 3, 128, 16>(a, grid, s);
     else
       wide ? launch_small_conv_cfg<64, 3, 64, 8>(a, grid, s) : launch_small_conv_cfg<32, 3, 64, 8>(a, grid, s);
-  } else {
+  } else if (K == 5) {
     wide ? launch_small_conv_cfg<64, 5, 64, 8>(a, grid, s) : launch_small_conv_cfg<32, 5, 64, 8>(a, grid, s);
+  } else {
+    wide ? launch_small_conv_cfg<64, 7, 64, 8>(a, grid, s) : launch_small_conv_cfg<32, 7, 64, 8>(a, grid, s);
   }
   check_launch("conv_small");
   return true;

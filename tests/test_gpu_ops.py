@@ -84,12 +84,14 @@ def test_conv1d_1x1_small_gemm(ops, B, C, O, T):
     (1, 64, 32, 300, 3, (2, 0)), # left padding only
     (1, 128, 100, 777, 5, 2),    # C_out not a multiple of 32
     (1, 512, 256, 130, 3, 1),    # 128-channel chunks at the smallest C_in
+    (1, 192, 512, 1000, 7, 3),   # decoder conv_pre at config 2
+    (2, 192, 512, 37, 7, 3),     # conv_pre, ragged short chunks, batch 2
     (1, 768, 192, 1000, 1, 0),   # enc_p phone embedding
     (2, 768, 2304, 499, 1, 0),   # HuBERT qkv at 10 s, batch 2
     (1, 3072, 768, 499, 1, 0),   # HuBERT FFN output
 ])
 def test_conv1d_small_chunked(ops, B, C, O, T, K, pad):
-    """K = 3 / 5 convs and wide 1x1 GEMMs on short sequences run the chunked
+    """K = 3 / 5 / 7 convs and wide 1x1 GEMMs on short sequences run the chunked
     whole-reduction kernel (no split-K): against the oracle at rel L2 1e-4,
     the first columns also against the float64 loops."""
     rng = np.random.default_rng(B * 7 + C + O + T)
