@@ -751,7 +751,7 @@ struct Synth : SessionBase {
       }
       if (keep_stages) {
         float* keep = buf("dec_stage" + std::to_string(i), (size_t)B * CL);
-        launch_copy(keep, A, B * CL, s);
+        run("dec.keep", 0.0, 8.0 * B * CL, [&] { launch_copy(keep, A, B * CL, s); });
       }
       cur = A;
       L = Lo;
@@ -957,6 +957,7 @@ int32_t rvc_synth_prep(int64_t sh, const float* phone, const int64_t* pitch, con
     s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
     const float* z = s.enc_flow_from(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P,
                                      (int)flow_head, g);
+    s.close_span();  // the phase scan below is no part of the flow's timing
     if (phase_out) {
       float* d_f0 = s.buf("in_f0", (size_t)(B * P));
       float* d_phase = s.buf("prep_phase", (size_t)(B * P));
@@ -964,7 +965,6 @@ int32_t rvc_synth_prep(int64_t sh, const float* phone, const int64_t* pitch, con
       launch_sine_phase(d_f0, d_phase, (int)B, (int)P, s.upp, (float)s.sr, 0, st);
       RVC_HIP(hipMemcpyAsync(phase_out, d_phase, sizeof(float) * B * P, hipMemcpyDeviceToHost, st));
     }
-    s.close_span();
     RVC_HIP(hipMemcpyAsync(z_out, z, sizeof(float) * B * s.H * Pf, hipMemcpyDeviceToHost, st));
     if (g_out) RVC_HIP(hipMemcpyAsync(g_out, g, sizeof(float) * B * s.gin, hipMemcpyDeviceToHost, st));
     RVC_HIP(hipStreamSynchronize(st));
