@@ -413,10 +413,27 @@ __device__ __forceinline__ void persist_tile(int lin, int n_tx, int n_ty, int& t
   }
 }
 
+// Direct-to-LDS buffer loads: lane i of the wave writes its 4 (16) bytes at
+// lds + 4 i (16 i); `lds` is the same for the whole wave.
+__device__ __forceinline__ void buffer_load_lds_b32(__amdgpu_buffer_rsrc_t r, float* lds, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, off, 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t r, float4* lds, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
+
 // FAM only names the instantiation (1: the three-group stored launches of
 // the decoder ResBlocks), so profiles can tell them from the other launches
 // of the same tile; the code is identical.
-template <int BM, int BN, int WM, int WN, int BK, int FAM>
+//
+// DIRECT (launches whose input takes no activation): chunks are staged by
+// direct-to-LDS buffer loads (lane i of a wave writes 4 or 16 bytes at the
+// wave's LDS base + 4i or 16i; out-of-range lanes write 0), so the staged
+// values never pass through registers.  A staging buffer then holds XREG
+// floats of x (every thread's XPT values: the window of the widest halo) and
+// WREG4 float4 of weights (the largest tap count's block); each wave waits
+// for its own loads before the chunk's barrier.
+template <int BM, int BN, int WM, int WN, int BK, int FAM, bool DIRECT = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(4)))
 void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floats, int cpx) {
@@ -424,6 +441,11 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = BK;
   constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
   static_assert(BK % 4 == 0 && (BK / 2) % 2 == 0, "channel chunk must be a multiple of 4");
+  constexpr int XREG = XPT * NT;
+  constexpr int WREG4 = kConvTapsMax * BKT * W4ROW;
+  // the weight loads past WREG4 (the last round only) skip whole waves
+  static_assert(!DIRECT || ((WPT - 1) * NT < WREG4 && WPT * NT >= WREG4 && (WREG4 - (WPT - 1) * NT) % 64 == 0),
+                "direct staging: weight rounds");
 
   const int per_b = n_tx * n_ty;
   const int per_group = a.B * per_b;
@@ -525,6 +547,22 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     for (int e = 0; e < WPT; ++e)
       wreg[e] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wo[e], 0, 0));
   };
+  auto gload_lds = [&](int ci0, int nb) {
+    const unsigned xr = 4u * (unsigned)((a.C_in - ci0 - 1) * (int)a.xc + a.L_in);
+    const unsigned wr = 4u * (unsigned)(((s_K - 1) * a.C_in + a.C_in - ci0) * a.w_ld);
+    const __amdgpu_buffer_rsrc_t xrs = uniform_rsrc(s_x + (long long)ci0 * a.xc, xr);
+    const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(s_w + (long long)ci0 * a.w_ld, wr);
+    float* xs = smem + nb * stage_floats;
+    float4* ws4 = reinterpret_cast<float4*>(xs + XREG);
+    const int wb = wave * 64;
+#pragma unroll
+    for (int e = 0; e < XPT; ++e) buffer_load_lds_b32(xrs, xs + e * NT + wb, xo[e]);
+#pragma unroll
+    for (int e = 0; e < WPT; ++e)
+      if (e + 1 < WPT || e * NT + wb < WREG4) buffer_load_lds_b128(wrs, ws4 + e * NT + wb, wo[e]);
+  };
+  // every load of this wave (direct-to-LDS ones included) has landed
+  auto wait_loads = [&]() { __builtin_amdgcn_s_waitcnt(0); };
   auto lstore = [&](int buf) {
     float* xs = smem + buf * stage_floats;
     float* ws = xs + BKT * s_XW;
@@ -551,7 +589,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   floatx16 acc[TM][TN];
   auto mfma_chunk = [&](int buf, int K, int dil, int XW) {
     const float* xs = smem + buf * stage_floats;
-    const float* ws = xs + BKT * XW;
+    const float* ws = xs + (DIRECT ? XREG : BKT * XW);
     const float* wbase = ws + half * BM + wm * WM + l32;
     const float* xbase = xs + half * XW + wn * WN + l32;
     float av[2][TM], bv[2][TN];
@@ -584,8 +622,13 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   };
 
   setup(item);
-  gload(0);
-  lstore(0);
+  if (DIRECT) {
+    gload_lds(0, 0);
+    wait_loads();
+  } else {
+    gload(0);
+    lstore(0);
+  }
   __syncthreads();
   int buf = 0;
   while (item < n_items) {
@@ -613,9 +656,15 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     // other buffer was last read in the previous chunk, which every wave
     // finished before the previous barrier.
     for (int c = 0; c + 1 < nchunk; ++c) {
-      gload((c + 1) * BKT);
+      if (DIRECT)
+        gload_lds((c + 1) * BKT, buf ^ 1);
+      else
+        gload((c + 1) * BKT);
       mfma_chunk(buf, c_K, c_dil, c_XW);
-      lstore(buf ^ 1);
+      if (DIRECT)
+        wait_loads();
+      else
+        lstore(buf ^ 1);
       if (c == 0) publish();
       __syncthreads();
       buf ^= 1;
@@ -628,7 +677,10 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     const bool more = next < n_items;
     if (more) {
       setup(next);
-      gload(0);
+      if (DIRECT)
+        gload_lds(0, buf ^ 1);
+      else
+        gload(0);
     }
     // Epilogue addressing through buffer resources over this batch item's
     // output / residual: lane offset (co_l, t) per column, the row within the
@@ -664,7 +716,10 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
           }
     }
     mfma_chunk(buf, c_K, c_dil, c_XW);
-    if (more) lstore(buf ^ 1);
+    if (DIRECT)
+      wait_loads();
+    else if (more)
+      lstore(buf ^ 1);
     __syncthreads();
     buf ^= 1;
 
@@ -1177,16 +1232,58 @@ bool persist_ok(const ConvLaunch& a) {
   return true;
 }
 
+template <int BM, int BN, int WM, int WN, int BK, bool DIRECT>
+bool launch_persist_kernel(const ConvLaunch& a, hipStream_t s, int stage, size_t lds, int n_tx, int n_ty, bool fam,
+                           long long items) {
+  using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
+  const void* kern = fam ? reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT>)
+                         : reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT>);
+  // 64 KiB of staging plus the kernel's static ticket word: allow the
+  // dynamic part its full size (a CU holds 160 KiB)
+  if (lds > 65536 - 256) {
+    static bool attr = false;  // per instantiation
+    if (!attr) {
+      RVC_HIP(hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit));
+      RVC_HIP(hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit));
+      attr = true;
+    }
+  }
+  const int per_cu = resident_blocks(kern, C::NT, lds);
+  if (per_cu < 1) return false;
+  long long grid = (long long)per_cu * device_cus();
+  if (grid >= 8) grid -= grid % 8;  // item j then runs on XCD j % 8
+  grid = std::min(grid, items);
+  const int cpx = device_cus() % 8 == 0 ? device_cus() / 8 : 0;  // CUs per XCD
+  if (fam)
+    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT>), dim3((unsigned)grid), dim3(C::NT),
+                       lds, s, a, n_tx, n_ty, stage, cpx);
+  else
+    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT>), dim3((unsigned)grid), dim3(C::NT),
+                       lds, s, a, n_tx, n_ty, stage, cpx);
+  check_launch("conv1d_mfma_persist");
+  return true;
+}
+
 template <int BM, int BN, int WM, int WN, int BK>
 bool launch_persist(const ConvLaunch& a, hipStream_t s) {
   using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
   if (a.C_out % BM != 0) return false;  // the epilogue has no row guard
-  int stage = 0;  // floats per staging buffer: the largest group
-  for (int g = 0; g < a.n_groups; ++g) {
-    const int XW = BN + (a.g[g].K - 1) * a.g[g].dil;
-    stage = std::max(stage, BK * XW + a.g[g].K * BK * BM);
+  // inputs that take no activation are staged by direct-to-LDS loads
+  const bool direct = a.in_act == ACT_NONE;
+  int stage = 0;  // floats per staging buffer
+  if (direct) {
+    stage = C::XPT * C::NT + kConvTapsMax * BK * BM;
+  } else {
+    for (int g = 0; g < a.n_groups; ++g) {  // the largest group
+      const int XW = BN + (a.g[g].K - 1) * a.g[g].dil;
+      stage = std::max(stage, BK * XW + a.g[g].K * BK * BM);
+    }
+    stage = (stage + 3) / 4 * 4;  // keeps each buffer's weight block 16-byte aligned
   }
-  stage = (stage + 3) / 4 * 4;  // keeps each buffer's weight block 16-byte aligned
   const size_t lds = 2 * sizeof(float) * (size_t)stage;
   if (lds > kLdsLimit) return false;
   const int n_tx = (max_n_out(a) + BN - 1) / BN;
@@ -1195,22 +1292,8 @@ bool launch_persist(const ConvLaunch& a, hipStream_t s) {
   RVC_CHECK(items < (1LL << 30), "conv1d_mfma: launch too large");
   bool fam = a.n_groups == 3;
   for (int g = 0; g < a.n_groups; ++g) fam = fam && a.g[g].combine == COMB_STORE;
-  const void* kern = fam ? reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1>)
-                         : reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0>);
-  const int per_cu = resident_blocks(kern, C::NT, lds);
-  if (per_cu < 1) return false;
-  long long grid = (long long)per_cu * device_cus();
-  if (grid >= 8) grid -= grid % 8;  // item j then runs on XCD j % 8
-  grid = std::min(grid, items);
-  const int cpx = device_cus() % 8 == 0 ? device_cus() / 8 : 0;  // CUs per XCD
-  if (fam)
-    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1>), dim3((unsigned)grid), dim3(C::NT), lds,
-                       s, a, n_tx, n_ty, stage, cpx);
-  else
-    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0>), dim3((unsigned)grid), dim3(C::NT), lds,
-                       s, a, n_tx, n_ty, stage, cpx);
-  check_launch("conv1d_mfma_persist");
-  return true;
+  return direct ? launch_persist_kernel<BM, BN, WM, WN, BK, true>(a, s, stage, lds, n_tx, n_ty, fam, items)
+                : launch_persist_kernel<BM, BN, WM, WN, BK, false>(a, s, stage, lds, n_tx, n_ty, fam, items);
 }
 
 // Split-K plan for a single-group stride-1 launch whose output tiles alone
