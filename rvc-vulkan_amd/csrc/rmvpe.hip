@@ -578,6 +578,7 @@ void launch_logmel_image(const float* M, int F, int Fp, int n_mels, float bn_s, 
 namespace {
 constexpr int kGruGroups = 16;
 constexpr int kGruUnits = 16;  // per workgroup
+constexpr int kGruPollSleep = 1;  // s_sleep units (64 clocks) between two polls
 
 __device__ __forceinline__ unsigned long long gru_word(int tag, float v) {
   return ((unsigned long long)(unsigned)tag << 32) | (unsigned long long)__float_as_uint(v);
@@ -600,6 +601,8 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
   const int ub = gw * kGruUnits + wave * 4;
   if (ub >= H) return;  // wave-uniform; no workgroup barrier below
   const float* W = g.whh + (long long)d * 3 * H * H;
+  // rows u * 3 + q: unit u's gates r, z, n side by side, so the reduction
+  // below leaves unit u's three sums in lanes 16 u .. 16 u + 15
   float wr[12][4];
 #pragma unroll
   for (int q = 0; q < 3; ++q)
@@ -608,17 +611,18 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int j = ub + u, col = 4 * lane + c;
-        wr[q * 4 + u][c] = (j < H && col < H) ? W[(long long)(q * H + j) * H + col] : 0.f;
+        wr[u * 3 + q][c] = (j < H && col < H) ? W[(long long)(q * H + j) * H + col] : 0.f;
       }
-  const int u = lane & 3;
+  const int u = lane >> 4;
   const int ju = ub + u;
-  const bool owner = lane < 4 && ju < H;
+  const bool owner = (lane & 15) == 0 && ju < H;
   float bh[3];
 #pragma unroll
   for (int q = 0; q < 3; ++q) bh[q] = owner ? g.bhh[(long long)d * 3 * H + q * H + ju] : 0.f;
   unsigned long long* st = g.state + d * 2 * 256;
   unsigned* err = g.sync + 2;
 
+  float hj = 0.f;  // the owner's h_{s-1} (h_{-1} = 0)
   for (int s = 0; s < g.T; ++s) {
     const int t = d == 0 ? s : g.T - 1 - s;
     // gate inputs of this step: issued before the wait
@@ -629,55 +633,65 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
       gxz = gp[(long long)(H + ju) * g.g_r];
       gxn = gp[(long long)(2 * H + ju) * g.g_r];
     }
-    // wait for h_{s-1}: all H words of buffer (s-1)&1 tagged s-1
+    // wait for h_{s-1}: all H words of buffer (s-1)&1 tagged s-1.  Every
+    // poll issues the lane's four word loads and the error-flag load
+    // together (one memory round trip per poll); columns past H read word
+    // H - 1, whose tag is awaited like the others (their weights are 0).
     const unsigned long long* hb = st + ((s - 1) & 1) * 256;
     const unsigned want = (unsigned)(s - 1);
     unsigned long long wv[4];
-    bool ready = true;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int col = 4 * lane + c;
-      wv[c] = col < H ? __hip_atomic_load(hb + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : gru_word(want, 0.f);
-      ready = ready && (unsigned)(wv[c] >> 32) == want;
-    }
     long long polls = 0;
-    while (!__all(ready)) {
-      if (++polls > g.spin_limit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+    for (;;) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        wv[c] = __hip_atomic_load(hb + min(4 * lane + c, H - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned ev = polls > 0 ? __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      bool ready = true;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ready = ready && (unsigned)(wv[c] >> 32) == want;
+      if (__all(ready)) break;
+      if (++polls > g.spin_limit || ev != 0u) {
         __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
       }
-      __builtin_amdgcn_s_sleep(1);
-      ready = true;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int col = 4 * lane + c;
-        if (col < H && (unsigned)(wv[c] >> 32) != want)
-          wv[c] = __hip_atomic_load(hb + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ready = ready && (col >= H || (unsigned)(wv[c] >> 32) == want);
-      }
+      __builtin_amdgcn_s_sleep(kGruPollSleep);
     }
     float hv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) hv[c] = __uint_as_float((unsigned)wv[c]);
-    // h_{s-1} of this lane's unit (word ju = ub + u sits in lane ub/4, element u)
-    const int src = ub >> 2;
-    const float h0 = __shfl(hv[0], src), h1 = __shfl(hv[1], src), h2 = __shfl(hv[2], src), h3 = __shfl(hv[3], src);
-    const float hj = u == 0 ? h0 : u == 1 ? h1 : u == 2 ? h2 : h3;
     float p[12];
 #pragma unroll
     for (int i = 0; i < 12; ++i) p[i] = ((wr[i][0] * hv[0] + wr[i][1] * hv[1]) + wr[i][2] * hv[2]) + wr[i][3] * hv[3];
+    // Sums over the 64 lanes, reduce-scatter style: across lanes 32 apart a
+    // lane keeps half of the rows (its partner's half of them added), across
+    // lanes 16 apart half of those, then the last three rows over the
+    // remaining 16 lanes -- 21 shuffles for the 12 sums.  Lane l ends with the
+    // rows 3 (l >> 4) .. + 2, the same value in every lane of its 16.
+    const bool hi32 = (lane & 32) != 0, hi16 = (lane & 16) != 0;
+    float a6[6], a3[3];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
+    for (int k = 0; k < 6; ++k) {
+      const float send = hi32 ? p[k] : p[k + 6];
+      const float keep = hi32 ? p[k + 6] : p[k];
+      a6[k] = keep + __shfl_xor(send, 32);
+    }
 #pragma unroll
-      for (int i = 0; i < 12; ++i) p[i] += __shfl_xor(p[i], off);
+    for (int k = 0; k < 3; ++k) {
+      const float send = hi16 ? a6[k] : a6[k + 3];
+      const float keep = hi16 ? a6[k + 3] : a6[k];
+      a3[k] = keep + __shfl_xor(send, 16);
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) a3[k] += __shfl_xor(a3[k], off);
     if (owner) {
-      const float sr = u == 0 ? p[0] : u == 1 ? p[1] : u == 2 ? p[2] : p[3];
-      const float sz = u == 0 ? p[4] : u == 1 ? p[5] : u == 2 ? p[6] : p[7];
-      const float sn = u == 0 ? p[8] : u == 1 ? p[9] : u == 2 ? p[10] : p[11];
+      const float sr = a3[0], sz = a3[1], sn = a3[2];
       const float r = sigmoid_as(gxr + (sr + bh[0]));
       const float zz = sigmoid_as(gxz + (sz + bh[1]));
       const float nn = tanhf(gxn + r * (sn + bh[2]));
       const float h = (1.0f - zz) * nn + zz * hj;
+      hj = h;  // h_{s-1} of this unit at the next step: the owner's own word
       __hip_atomic_store(st + (s & 1) * 256 + ju, gru_word(s, h), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       g.out[d * g.o_d + (long long)t * g.o_t + (long long)ju * g.o_j] = h;
     }
