@@ -662,29 +662,33 @@ __global__ __launch_bounds__(256) void bigru_kernel(GruArgs g) {
     float p[12];
 #pragma unroll
     for (int i = 0; i < 12; ++i) p[i] = ((wr[i][0] * hv[0] + wr[i][1] * hv[1]) + wr[i][2] * hv[2]) + wr[i][3] * hv[3];
-    // Sums over the 64 lanes, reduce-scatter style: across lanes 32 apart a
-    // lane keeps half of the rows (its partner's half of them added), across
-    // lanes 16 apart half of those, then the last three rows over the
-    // remaining 16 lanes -- 21 shuffles for the 12 sums.  Lane l ends with the
-    // rows 3 (l >> 4) .. + 2, the same value in every lane of its 16.
-    const bool hi32 = (lane & 32) != 0, hi16 = (lane & 16) != 0;
+    // Sums over the 64 lanes, reduce-scatter style, without LDS: a
+    // permlane32 swap of rows k and k + 6 leaves lanes 0-31 with row k of
+    // lanes l, l + 32 and lanes 32-63 with row k + 6 (the two halves added),
+    // a permlane16 swap does the same across 16-lane rows, and DPP mirrors
+    // and quad permutations add the last three rows over their 16 lanes.
+    // Lane l ends with the rows 3 (l >> 4) .. + 2, the same value in every
+    // lane of its 16 (each pair adds the same two terms).
     float a6[6], a3[3];
 #pragma unroll
     for (int k = 0; k < 6; ++k) {
-      const float send = hi32 ? p[k] : p[k + 6];
-      const float keep = hi32 ? p[k + 6] : p[k];
-      a6[k] = keep + __shfl_xor(send, 32);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[k]), __float_as_uint(p[k + 6]), false, false);
+      a6[k] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      const float send = hi16 ? a6[k] : a6[k + 3];
-      const float keep = hi16 ? a6[k + 3] : a6[k];
-      a3[k] = keep + __shfl_xor(send, 16);
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(a6[k]), __float_as_uint(a6[k + 3]), false, false);
+      a3[k] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
+    // row_mirror (l <-> 15 - l), row_half_mirror (l <-> 7 - l), then the
+    // quad permutations [2,3,0,1] and [1,0,3,2]
 #pragma unroll
-    for (int off = 8; off >= 1; off >>= 1)
-#pragma unroll
-      for (int k = 0; k < 3; ++k) a3[k] += __shfl_xor(a3[k], off);
+    for (int k = 0; k < 3; ++k) {
+      a3[k] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a3[k]), 0x140, 0xF, 0xF, false));
+      a3[k] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a3[k]), 0x141, 0xF, 0xF, false));
+      a3[k] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a3[k]), 0x4E, 0xF, 0xF, false));
+      a3[k] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a3[k]), 0xB1, 0xF, 0xF, false));
+    }
     if (owner) {
       const float sr = a3[0], sz = a3[1], sn = a3[2];
       const float r = sigmoid_as(gxr + (sr + bh[0]));
