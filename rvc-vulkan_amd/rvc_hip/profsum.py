@@ -90,7 +90,10 @@ def pmc_rows(db: str):
 
 def is_resblock(kernel: str, grid) -> bool:
     if kernel.startswith("conv1d_mfma_persist_kernel"):
-        return kernel.replace(" ", "").endswith(",1>")   # FAM = 1: the three-group stored launches
+        # template arguments <BM, BN, WM, WN, BK, FAM[, DIRECT]>: FAM = 1 marks
+        # the three-group stored launches
+        args = kernel[kernel.find("<") + 1:kernel.rfind(">")].replace(" ", "").split(",")
+        return len(args) >= 6 and args[5] == "1"
     return kernel.startswith("conv1d_mfma_kernel") and grid[2] == 3 and grid[0] >= 64
 
 

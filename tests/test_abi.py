@@ -203,3 +203,17 @@ def test_new_exports_reject_bad_handles(hip):
     assert L.rvc_rmvpe_create(424242) == -1
     assert L.rvc_rmvpe_finalize(424242) == -1
     assert hip.last_error() == "invalid rmvpe handle"
+
+
+def test_profile_summary_resblock_family():
+    """The kernel-trace summary's ResBlock family: persistent instantiations
+    with FAM = 1 (sixth template argument, with or without the staging flag
+    after it) and three-group one-shot grids."""
+    from rvc_hip.profsum import is_resblock
+
+    assert is_resblock("conv1d_mfma_persist_kernel<64, 256, 32, 64, 8, 1, true>", (512, 1, 1))
+    assert is_resblock("conv1d_mfma_persist_kernel<32, 512, 32, 64, 8, 1, false>", (512, 1, 1))
+    assert is_resblock("conv1d_mfma_persist_kernel<32, 256, 32, 64, 8, 1>", (960, 1, 1))
+    assert not is_resblock("conv1d_mfma_persist_kernel<64, 256, 32, 64, 8, 0, true>", (512, 1, 1))
+    assert is_resblock("conv1d_mfma_kernel<64, 128, 32, 64, 8, 1, 1, 11, 1>", (79, 2, 3))
+    assert not is_resblock("conv1d_mfma_kernel<64, 128, 32, 64, 8, 1, 1, 11, 1>", (79, 2, 1))
