@@ -532,9 +532,10 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     }
   };
   float xv[XPT];
-  float4 wreg[WPT];
-  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  auto gload = [&](int ci0) {
+  // Register staging of x (the leaky ReLU is applied on the way to LDS);
+  // the weights need no transform and go straight into buffer nb's weight
+  // block (direct-to-LDS loads, lanes past the item's taps masked).
+  auto gload = [&](int ci0, int nb) {
     // ranges: rows ci0.. of x ((C_in - ci0 - 1) full rows + one of L_in), and
     // the weight rows k * C_in + ci0 + rr of every tap
     const unsigned xr = 4u * (unsigned)((a.C_in - ci0 - 1) * (int)a.xc + a.L_in);
@@ -543,9 +544,12 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(s_w + (long long)ci0 * a.w_ld, wr);
 #pragma unroll
     for (int e = 0; e < XPT; ++e) xv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xo[e], 0, 0));
+    float4* ws4 = reinterpret_cast<float4*>(smem + nb * stage_floats + BKT * s_XW);
+    const int nw4 = s_K * BKT * W4ROW;
+    const int wb = wave * 64;
 #pragma unroll
     for (int e = 0; e < WPT; ++e)
-      wreg[e] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wo[e], 0, 0));
+      if (tid + e * NT < nw4) buffer_load_lds_b128(wrs, ws4 + e * NT + wb, wo[e]);
   };
   auto gload_lds = [&](int ci0, int nb) {
     const unsigned xr = 4u * (unsigned)((a.C_in - ci0 - 1) * (int)a.xc + a.L_in);
@@ -565,9 +569,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   auto wait_loads = [&]() { __builtin_amdgcn_s_waitcnt(0); };
   auto lstore = [&](int buf) {
     float* xs = smem + buf * stage_floats;
-    float* ws = xs + BKT * s_XW;
     const int nx = BKT * s_XW;
-    const int nw4 = s_K * BKT * W4ROW;
 #pragma unroll
     for (int e = 0; e < XPT; ++e) {
       const int idx = tid + e * NT;
@@ -576,11 +578,6 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
         if (a.in_act == ACT_LEAKY) v = v >= 0.f ? v : v * a.in_slope;
         xs[idx] = v;
       }
-    }
-#pragma unroll
-    for (int e = 0; e < WPT; ++e) {
-      const int idx = tid + e * NT;
-      if (idx < nw4) reinterpret_cast<float4*>(ws)[idx] = wreg[e];
     }
   };
 
@@ -626,8 +623,9 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     gload_lds(0, 0);
     wait_loads();
   } else {
-    gload(0);
+    gload(0, 0);
     lstore(0);
+    wait_loads();
   }
   __syncthreads();
   int buf = 0;
@@ -659,12 +657,10 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
       if (DIRECT)
         gload_lds((c + 1) * BKT, buf ^ 1);
       else
-        gload((c + 1) * BKT);
+        gload((c + 1) * BKT, buf ^ 1);
       mfma_chunk(buf, c_K, c_dil, c_XW);
-      if (DIRECT)
-        wait_loads();
-      else
-        lstore(buf ^ 1);
+      if (!DIRECT) lstore(buf ^ 1);
+      wait_loads();
       if (c == 0) publish();
       __syncthreads();
       buf ^= 1;
@@ -680,7 +676,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
       if (DIRECT)
         gload_lds(0, buf ^ 1);
       else
-        gload(0);
+        gload(0, buf ^ 1);
     }
     // Epilogue addressing through buffer resources over this batch item's
     // output / residual: lane offset (co_l, t) per column, the row within the
@@ -716,10 +712,8 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
           }
     }
     mfma_chunk(buf, c_K, c_dil, c_XW);
-    if (DIRECT)
-      wait_loads();
-    else if (more)
-      lstore(buf ^ 1);
+    if (!DIRECT && more) lstore(buf ^ 1);
+    wait_loads();
     __syncthreads();
     buf ^= 1;
 
