@@ -413,15 +413,6 @@ __device__ __forceinline__ void persist_tile(int lin, int n_tx, int n_ty, int& t
   }
 }
 
-// Direct-to-LDS buffer loads: lane i of the wave writes its 4 (16) bytes at
-// lds + 4 i (16 i); `lds` is the same for the whole wave.
-__device__ __forceinline__ void buffer_load_lds_b32(__amdgpu_buffer_rsrc_t r, float* lds, unsigned off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, off, 0, 0, 0);
-}
-__device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t r, float4* lds, unsigned off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
-}
-
 // FAM only names the instantiation (1: the three-group stored launches of
 // the decoder ResBlocks), so profiles can tell them from the other launches
 // of the same tile; the code is identical.

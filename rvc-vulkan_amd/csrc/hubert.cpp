@@ -37,6 +37,7 @@ struct Hubert : SessionBase {
   float *fp_ln_g = nullptr, *fp_ln_b = nullptr, *fp_w = nullptr, *fp_b = nullptr;
   std::vector<float*> pos_w;              // per tap block: pos_groups packed slabs [Kb][cpg][ld]
   std::vector<int> pos_k0, pos_kb;
+  float* pos_wl = nullptr;                // [groups][K][cpg in][cpg out] for the one-launch kernel
   float *pos_b = nullptr, *enc_ln_g = nullptr, *enc_ln_b = nullptr;
   struct Layer {
     float *wqkv, *bqkv, *wo, *bo, *ln1_g, *ln1_b, *wi, *bi, *wf, *bf, *ln2_g, *ln2_b;
@@ -112,8 +113,18 @@ struct Hubert : SessionBase {
       for (long long i = 0; i < (long long)H * cpg; ++i)
         wpos[i * pos_k + k] = g.data[k] * (v.data[i * pos_k + k] / nrm);
     }
+    if (posconv_supported(cpg, pos_k, pos_k / 2)) {
+      std::vector<float> wl((size_t)pos_groups * pos_k * cpg * cpg);
+      for (int gi = 0; gi < pos_groups; ++gi)
+        for (int k = 0; k < pos_k; ++k)
+          for (int ci = 0; ci < cpg; ++ci)
+            for (int co = 0; co < cpg; ++co)
+              wl[(((size_t)gi * pos_k + k) * cpg + ci) * cpg + co] =
+                  wpos[(((size_t)gi * cpg + co) * cpg + ci) * pos_k + k];
+      pos_wl = upload(wl);
+    }
     const int ld = packed_ld(cpg);
-    for (int k0 = 0; k0 < pos_k; k0 += kTapBlock) {
+    for (int k0 = 0; pos_wl == nullptr && k0 < pos_k; k0 += kTapBlock) {
       const int kb = std::min(kTapBlock, pos_k - k0);
       std::vector<float> blk((size_t)pos_groups * kb * cpg * ld, 0.f);
       for (int gi = 0; gi < pos_groups; ++gi) {
@@ -226,6 +237,11 @@ struct Hubert : SessionBase {
     conv("hub.proj", c1x1(lnf, (long long)C * L, fp_w, fp_b, proj, B, C, H, (int)L));
     // ---- positional conv in tap blocks (padding pos_k/2, the right column dropped)
     float* pos = buf("pos", (size_t)B * HL);
+    if (pos_wl) {
+      run("hub.pos", 2.0 * B * (double)H * cpg * pos_k * L,
+          4.0 * (2.0 * B * HL + (double)pos_groups * pos_k * cpg * cpg),
+          [&] { launch_posconv(proj, pos_wl, pos_b, pos, B, H, (int)L, cpg, pos_k, pos_k / 2, s); });
+    }
     for (size_t j = 0; j < pos_w.size(); ++j) {
       const int kb = pos_kb[j];
       ConvLaunch pl{};

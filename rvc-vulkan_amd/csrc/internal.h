@@ -59,6 +59,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const void* base,
 }
 // the offset a masked lane passes: above every range these kernels build
 constexpr unsigned kBufOut = 0x80000000u;
+// Direct-to-LDS buffer loads: lane i of the wave writes its 4 (16) bytes at
+// lds + 4 i (16 i), an out-of-range lane writes 0; `lds` is the same for the
+// whole wave.  The wave waits for them with s_waitcnt vmcnt before a barrier.
+__device__ __forceinline__ void buffer_load_lds_b32(__amdgpu_buffer_rsrc_t r, float* lds, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4, off, 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t r, float4* lds, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
 
 // logistic function in the two-branch form of runtime/nn.py:520-523
 __device__ inline float sigmoid_as(float x) {
@@ -296,6 +305,11 @@ void launch_mul(float* c, const float* a, const float* b, long long n, hipStream
 void launch_fill(float* a, long long n, float v, hipStream_t s);
 // out = a + gelu(p)
 void launch_add_gelu(float* out, const float* a, const float* p, long long n, hipStream_t s);
+// HuBERT's grouped long positional conv (posconv.hip): x, out [B][H][L],
+// w [H / cpg][K][cpg (in)][cpg (out)], bias [H]; out[t] reads x[t + k - pad]
+bool posconv_supported(int cpg, int K, int pad);
+void launch_posconv(const float* x, const float* w, const float* bias, float* out, int B, int H, int L, int cpg,
+                    int K, int pad, hipStream_t s);
 // a = gelu(a) in place (erf form, gelu_as)
 void launch_gelu(float* a, long long n, hipStream_t s);
 // out[i] = a[i] + bias[i % cols]
