@@ -860,7 +860,7 @@ template <int BN>
 __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
   constexpr int TN = BN / 32;
   constexpr int RS = 256 / BN;        // input channels one pass of the workgroup stages
-  constexpr int LB = 16;              // loads in flight per thread per staging batch
+  constexpr int LB = 12;              // loads in flight per thread per staging batch
   constexpr unsigned kOut = 0x80000000u;
   extern __shared__ float smem[];
   const int b = blockIdx.z % a.B;
@@ -875,51 +875,64 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int C_in = a.C_in;
-  // LDS: ws [256][32] (rows past C_in zero), then xs [ceil(C_in / (RS*LB)) * RS*LB][BN]
-  // (rows past C_in zero): every staging load and store is unconditional, so
-  // the loads of a batch are all in flight before the first wait.
+  // LDS: ws [ceil32(C_in)][32] (rows past C_in zero), then xs
+  // [ceil(n_it / LB) * LB * RS][BN] (rows past C_in zero).  Sized to C_in, so
+  // a 192-channel reduction at BN = 32 takes 48 KiB and three workgroups fit a
+  // CU (enc_p's qkv conv: 576 workgroups in one round, 11.6 -> 9.3 us).
+  const int n_it = C_in / RS;  // C_in % 8 == 0, RS <= 8
   float* ws = smem;
-  float* xs = smem + 256 * 32;
+  float* xs = smem + ((C_in + 31) & ~31) * 32;
 
-  // weights first (8 float4 per thread), then x in batches of LB independent
-  // loads: thread tid always stages column tid % BN of rows tid / BN + RS * j,
-  // so the bounds test is one comparison per thread.
+  // the weights (8 float4 loads per thread, rows past C_in read as zero) and
+  // the first batch of x in flight together, then the rest of x in batches of
+  // LB independent loads: thread tid always stages column tid % BN of rows
+  // tid / BN + RS * j, so the bounds test is one comparison per thread.
   const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(G.w, 4u * (unsigned)(C_in * a.w_ld));
-  const int cols = (a.C_out + 3) & ~3;
-  {
-    const int ci = tid >> 3;
-    const int co = co0 + 4 * (tid & 7);
-    float4 wv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int c = ci + 32 * j;
-      const unsigned off = (c < C_in && co < cols) ? 4u * (unsigned)(c * a.w_ld + co) : kOut;
-      wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) reinterpret_cast<float4*>(ws)[tid + 256 * j] = wv[j];
-  }
   const __amdgpu_buffer_rsrc_t xrs =
       uniform_rsrc(G.x + (long long)b * a.xb, 4u * (unsigned)((C_in - 1) * (int)a.xc + a.L_in));
+  const int cols = (a.C_out + 3) & ~3;
   const int xcol = tid % BN;
   const int xrow = tid / BN;
   const bool xin = i0 + xcol < a.L_in;
-  const int n_it = C_in / RS;  // C_in % 8 == 0, RS <= 8
   const bool leaky = a.in_act == ACT_LEAKY;
-  for (int j0 = 0; j0 < n_it; j0 += LB) {
-    float v[LB];
+  // kOut + anything below 2^31 stays past the end of the buffer
+  const unsigned xbase = xin ? 4u * (unsigned)(xrow * (int)a.xc + i0 + xcol) : kOut;
+  const unsigned xstep = 4u * (unsigned)(RS * (int)a.xc);
+  auto xload = [&](int j0, float (&v)[LB]) {
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
-      const int ci = xrow + RS * (j0 + j);
-      const unsigned off = (xin && j0 + j < n_it) ? 4u * (unsigned)(ci * (int)a.xc + i0 + xcol) : kOut;
+      const unsigned off = j0 + j < n_it ? xbase + (unsigned)(j0 + j) * xstep : kOut;
       v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off, 0, 0));
     }
+  };
+  auto xstore = [&](int j0, const float (&v)[LB]) {
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
       float u = v[j];
       if (leaky) u = u >= 0.f ? u : u * a.in_slope;
       xs[(j0 + j) * 256 + tid] = u;
     }
+  };
+  float4 wv[8];
+  {
+    const int ci = tid >> 3;
+    const int co = co0 + 4 * (tid & 7);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = ci + 32 * j;
+      const unsigned off = (c < C_in && co < cols) ? 4u * (unsigned)(c * a.w_ld + co) : kOut;
+      wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+    }
+  }
+  for (int j0 = 0; j0 < n_it; j0 += LB) {
+    float v[LB];
+    xload(j0, v);
+    if (j0 == 0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (32 * j < C_in) reinterpret_cast<float4*>(ws)[tid + 256 * j] = wv[j];  // uniform
+    }
+    xstore(j0, v);
   }
   __syncthreads();
 
@@ -1405,15 +1418,20 @@ bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
   const long long z = (long long)a.n_groups * a.B;
   const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 320;  // as in launch_small_conv
   const int BN = wide ? 64 : 32;
-  const size_t n_it = (size_t)a.C_in / (256 / BN);  // staging passes, rounded up to the batch of 16
-  const size_t lds = sizeof(float) * (256 * 32 + (n_it + 15) / 16 * 16 * 256);
+  // ws: C_in rounded up to 32 rows of 32; xs: the staging passes rounded up
+  // to the batch of 12, 256 floats each; the epilogue's four waves' tiles
+  const size_t n_it = (size_t)a.C_in / (256 / BN);
+  const size_t lds = sizeof(float) * std::max(((size_t)a.C_in + 31) / 32 * 32 * 32 + (n_it + 11) / 12 * 12 * 256,
+                                              (size_t)4 * (BN / 32) * 1024);
+  constexpr int kMaxLds = sizeof(float) * (256 * 32 + 72 * 256);  // C_in = 256, BN = 64
+  RVC_CHECK(lds <= (size_t)kMaxLds, "conv1x1_small: LDS above its limit");
   const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
   static bool attr = false;
   if (!attr) {
     RVC_HIP(hipFuncSetAttribute((const void*)conv1x1_small_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(sizeof(float) * 256 * 96)));
+                                kMaxLds));
     RVC_HIP(hipFuncSetAttribute((const void*)conv1x1_small_kernel<32>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(sizeof(float) * 256 * 96)));
+                                kMaxLds));
     attr = true;
   }
   if (wide)
