@@ -54,9 +54,9 @@ struct AttnLds {
   static constexpr int V = AWAVES * ROWS * VSTRIDE;    // per-wave V tiles
   static constexpr int MERGE = (AWAVES - 1) * (DT * 16 * 64 + 2 * 32);
   static constexpr int R = 32 * 32;                    // R^T[r][t]
-  static constexpr int PB = AWAVES * 33 * 32;          // per-wave band probabilities [r][t] + a junk row
   static constexpr int VM = V > MERGE ? V : MERGE;
-  static constexpr int TOTAL = Q + VM + R + PB;
+  // then per wave the band probabilities [r][t], rows [0, nb) and a junk row nb
+  static size_t bytes(int nb) { return sizeof(float) * (Q + VM + R + AWAVES * (nb + 1) * 32); }
 };
 
 template <int DT>
@@ -90,6 +90,13 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   const int nb = emb_k != nullptr ? 2 * window + 1 : 0;  // no band: plain attention
   const int t = t0 + l32;
   const float sq = sqrtf((float)D);
+  // this workgroup's key tiles [kt_begin, kt_end); the band rows are needed
+  // only where the slice meets keys [t0 - window, t0 + 31 + window]
+  const int ntile = (P + 31) / 32;
+  const int per = (ntile + KS - 1) / KS;
+  const int kt_begin = ks * per;
+  const int kt_end = min(ntile, (ks + 1) * per);
+  const bool slice_near = nb > 0 && kt_begin * 32 <= t0 + 31 + window && kt_end * 32 - 1 >= t0 - window;
 
   // stage qs[d][t] = q[d][t0 + t] / sqrt(D)
   for (int e = tid; e < Lds::Q; e += 256) {
@@ -97,13 +104,13 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
     const unsigned off = (d < D && t0 + j < P) ? 4u * (unsigned)(d * P + t0 + j) : kBufOut;
     Qs[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(qrs, off, 0, 0)) / sq;
   }
-  // band probabilities per wave: rows [0, nb) live, row 32 takes the masked
+  // band probabilities per wave: rows [0, nb) live, row nb takes the masked
   // lanes' (zero) updates so every lane can store unconditionally
-  float* Pb = PbAll + wave * 33 * 32;
-  for (int e = lane; e < 33 * 32; e += 64) Pb[e] = 0.f;
+  float* Pb = PbAll + wave * (nb + 1) * 32;
+  for (int e = lane; e < (nb + 1) * 32; e += 64) Pb[e] = 0.f;
   __syncthreads();
   // R^T[r][t] = emb_k[r] . qs_t   (wave 0)
-  if (wave == 0) {
+  if (wave == 0 && slice_near) {
     const __amdgpu_buffer_rsrc_t ers = uniform_rsrc(emb_k, 4u * (unsigned)(nb * D));
     floatx16 racc;
 #pragma unroll
@@ -130,10 +137,7 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   float l = 0.f;        // running sum over this half-wave's key rows
   bool band_seen = false;  // wave-uniform: Pb holds probabilities to rescale
 
-  const int ntile = (P + 31) / 32;
-  const int per = (ntile + KS - 1) / KS;
-  const int kt_end = min(ntile, (ks + 1) * per);
-  for (int kt = ks * per + wave; kt < kt_end; kt += AWAVES) {
+  for (int kt = kt_begin + wave; kt < kt_end; kt += AWAVES) {
     const int s0 = kt * 32;
     // all global loads of the tile first: K operands and the V tile
     // K operand kk and V staging element i read the same lane position:
@@ -197,9 +201,10 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
 #pragma unroll
       for (int r = 0; r < 16; ++r) O[dt][r] *= alpha;
     if (band_seen) {
-      // the two half-waves rescale rows [0, 16) and [16, 32)
+      // the two half-waves rescale rows [0, 16) and [16, nb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) Pb[(16 * half + i) * 32 + l32] *= alpha;
+      for (int i = 0; i < 16; ++i)
+        if (16 * half + i < nb) Pb[(16 * half + i) * 32 + l32] *= alpha;
     }
     if (near) {
       band_seen = true;
@@ -207,7 +212,7 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
       for (int r = 0; r < 16; ++r) {
         const int rr = s0 + acc_row(r, half) - t + window;
         const bool in = (unsigned)rr < (unsigned)nb;
-        float* pe = Pb + (in ? rr : 32) * 32 + l32;
+        float* pe = Pb + (in ? rr : nb) * 32 + l32;
         *pe = *pe + (in ? S[r] : 0.f);
       }
     }
@@ -226,7 +231,7 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
     const __amdgpu_buffer_rsrc_t ers = uniform_rsrc(emb_v, 4u * (unsigned)(nb * D));
     for (int kk = 0; kk < (nb + 1) / 2; ++kk) {
       const int rr = 2 * kk + half;
-      const float bval = Pb[rr * 32 + l32];  // rows in [nb, 32) stay zero
+      const float bval = Pb[rr * 32 + l32];  // row nb (odd nb) stays zero
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int d = dt * 32 + l32;
@@ -300,7 +305,9 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   }
 }
 
-// out[b][h*D+d][t] = sum_ks O_ks e^(m_ks - M) / sum_ks l_ks e^(m_ks - M)
+// out[b][h*D+d][t] = sum_ks O_ks e^(m_ks - M) / sum_ks l_ks e^(m_ks - M), M the
+// largest m_ks: one pass over the slices with a running maximum (an empty
+// slice, m = -inf, carries no weight)
 __global__ __launch_bounds__(256) void relpos_attention_merge(const float* part, float* out, int H, int D, int P,
                                                               int KS, long long n) {
   const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -309,15 +316,29 @@ __global__ __launch_bounds__(256) void relpos_attention_merge(const float* part,
   const long long r = e / P;
   const int d = (int)(r % D);
   const long long bh = r / D;
-  const float* pb = part + bh * KS * (long long)(D + 2) * P;
-  float M = -INFINITY;
-  for (int k = 0; k < KS; ++k) M = fmaxf(M, pb[k * (long long)(D + 2) * P + t]);
-  float L = 0.f, O = 0.f;
-  for (int k = 0; k < KS; ++k) {
-    const float* s = pb + k * (long long)(D + 2) * P;
-    const float f = s[t] == -INFINITY ? 0.f : expf(s[t] - M);
-    L += s[P + t] * f;
-    O += s[(long long)(2 + d) * P + t] * f;
+  const long long slice = (long long)(D + 2) * P;
+  const float* pb = part + bh * KS * slice;
+  constexpr int U = 8;  // slices whose loads are in flight together
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int k0 = 0; k0 < KS; k0 += U) {
+    float mk[U], lk[U], ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float* s = pb + min(k0 + u, KS - 1) * slice;  // past KS: re-reads the last slice, skipped below
+      mk[u] = s[t];
+      lk[u] = s[P + t];
+      ok[u] = s[(long long)(2 + d) * P + t];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (k0 + u >= KS || mk[u] == -INFINITY) continue;
+      const float Mn = fmaxf(M, mk[u]);
+      const float fo = expf(M - Mn);  // 0 while M = -inf
+      const float fk = expf(mk[u] - Mn);
+      L = L * fo + lk[u] * fk;
+      O = O * fo + ok[u] * fk;
+      M = Mn;
+    }
   }
   out[(bh * D + d) * (long long)P + t] = O / L;
 }
@@ -325,11 +346,12 @@ __global__ __launch_bounds__(256) void relpos_attention_merge(const float* part,
 template <int DT>
 void launch_dt(const float* qkv, const float* emb_k, const float* emb_v, float* out, float* part, int B, int H,
                int D, int P, int window, int KS, hipStream_t s) {
-  const size_t lds = sizeof(float) * AttnLds<DT>::TOTAL;
+  const int nb = emb_k != nullptr ? 2 * window + 1 : 0;
+  const size_t lds = AttnLds<DT>::bytes(nb);
   static bool attr = false;
   if (!attr) {
     RVC_HIP(hipFuncSetAttribute((const void*)relpos_attention_kernel<DT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds));
+                                (int)AttnLds<DT>::bytes(2 * kMaxWindow + 1)));
     attr = true;
   }
   dim3 grid((P + 31) / 32, H, B * KS);
@@ -338,21 +360,49 @@ void launch_dt(const float* qkv, const float* emb_k, const float* emb_v, float* 
   check_launch("relpos_attention");
 }
 
+template <int DT>
+int blocks_per_cu(int nb) {
+  int n = 0;
+  RVC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, relpos_attention_kernel<DT>, 256, AttnLds<DT>::bytes(nb)));
+  return std::max(n, 1);
+}
+
+// workgroups of the attention kernel one CU holds at once (registers and LDS)
+// times the CUs, for head dim D and nb band rows
+int attention_resident_blocks(int D, int nb) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    RVC_HIP(hipGetDevice(&dev));
+    RVC_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  switch ((D + 31) / 32) {
+    case 1: return cus * blocks_per_cu<1>(nb);
+    case 2: return cus * blocks_per_cu<2>(nb);
+    case 3: return cus * blocks_per_cu<3>(nb);
+    default: return cus * blocks_per_cu<4>(nb);
+  }
+}
+
 }  // namespace
 
-// The key-split count depends on (H, P) only, never on B: the merge order of the
-// split partial sums is part of the result's rounding, so a batched call must use
+// The key split fills what the GPU holds at once (all CUs times the
+// workgroups one CU takes), each wave keeping at least one key tile.  It
+// depends on (H, D, P, window) only, never on B: the merge order of the split
+// partial sums is part of the result's rounding, so a batched call must use
 // the split a single chunk would, or batch != per-chunk bit for bit.
-int relpos_attention_splits(int /*B*/, int H, int P) {
+int relpos_attention_splits(int H, int D, int P, int window, bool band) {
+  const int nb = band ? 2 * window + 1 : 0;
+  const int per_gpu = attention_resident_blocks(D, nb);
   const int ntile = (P + 31) / 32;
-  const int blocks = ((P + 31) / 32) * H;
-  int ks = (256 + blocks - 1) / blocks;
+  const int blocks = ntile * H;
+  int ks = (per_gpu + blocks - 1) / blocks;
   ks = std::min(ks, std::max(1, ntile / AWAVES));
   return std::max(ks, 1);
 }
 
-size_t relpos_attention_scratch_floats(int B, int H, int D, int P) {
-  const int ks = relpos_attention_splits(B, H, P);
+size_t relpos_attention_scratch_floats(int B, int H, int D, int P, int window, bool band) {
+  const int ks = relpos_attention_splits(H, D, P, window, band);
   return ks > 1 ? (size_t)B * H * ks * (D + 2) * P : 0;
 }
 
@@ -368,7 +418,7 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
   // offset plus 63 row steps of 2P floats, stay below 2^31 / 2^32
   RVC_CHECK((long long)D * P * 4 < (1LL << 31) && 63LL * 8 * P < (1LL << 31),
             "relpos_attention: sequence too long for 32-bit offsets");
-  const int KS = relpos_attention_splits(B, H, P);
+  const int KS = relpos_attention_splits(H, D, P, window, emb_k != nullptr);
   RVC_CHECK(KS == 1 || scratch != nullptr, "relpos_attention: scratch buffer required");
   const int dt = (D + 31) / 32;
   if (dt == 1) launch_dt<1>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);

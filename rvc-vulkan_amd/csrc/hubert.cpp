@@ -274,7 +274,7 @@ struct Hubert : SessionBase {
     float* ff = buf("ffn", (size_t)B * F * L);
     float* xa = buf("xa", (size_t)B * HL);
     float* xb_ = buf("xb", (size_t)B * HL);
-    float* part = buf("attn_part", std::max<size_t>(1, relpos_attention_scratch_floats(B, kHeads, D, (int)L)));
+    float* part = buf("attn_part", std::max<size_t>(1, relpos_attention_scratch_floats(B, kHeads, D, (int)L, 0, false)));
     const float* cur = x0;
     const int nl = version == 1 ? 9 : n_layers;
     for (int i = 0; i < nl; ++i) {

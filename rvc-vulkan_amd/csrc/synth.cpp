@@ -415,7 +415,7 @@ struct Synth : SessionBase {
     float* att = buf("att", (size_t)B * HP);
     float* o = buf("enco", (size_t)B * HP);
     float* f = buf("ffn", (size_t)B * F * P);
-    float* apart = buf("attn_part", std::max<size_t>(1, relpos_attention_scratch_floats(B, heads, kc, P)));
+    float* apart = buf("attn_part", std::max<size_t>(1, relpos_attention_scratch_floats(B, heads, kc, P, kWindow, true)));
     const float* x = xin;
     for (int i = 0; i < n_layers; ++i) {
       const EncL& L = enc[i];
