@@ -1390,13 +1390,15 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
   // Waves per workgroup (each taking its share of every chunk's channels):
   // sixteen for the 128-channel 3-tap chunks (enc_p's FFN output conv, 768 x
-  // 3), eight for the other K-tap convs, four for the wide 1x1 GEMMs.
-  // Measured at config 2 against four waves: FFN output conv 24.6 -> 20.6 us
-  // (8) -> 18.8 us (16), WaveNet in-layer 18.2 -> 16.7 us, FFN input conv
-  // 19.3 -> 17.8 us.  A function of the shape only, never of B: the wave count
-  // sets the summation order.
+  // 3), eight for the other K-tap convs and the 1x1 GEMMs.  Measured at
+  // config 2 against four waves: FFN output conv 24.6 -> 20.6 us (8) -> 18.8
+  // us (16), WaveNet in-layer 18.2 -> 16.7 us, FFN input conv 19.3 -> 17.8 us;
+  // at config 3 the 32-column 1x1 GEMMs (out-proj, FFN output) 35.2 -> 32.3 us
+  // (8) / 31.0 us (16, but the 64-column ones 39 -> 43 us).  A function of the
+  // shape only, never of B or the tile width (which depends on B): the wave
+  // count sets the summation order.
   if (K == 1) {
-    wide ? launch_small_conv_cfg<64, 1, 128, 4>(a, grid, s) : launch_small_conv_cfg<32, 1, 128, 4>(a, grid, s);
+    wide ? launch_small_conv_cfg<64, 1, 128, 8>(a, grid, s) : launch_small_conv_cfg<32, 1, 128, 8>(a, grid, s);
   } else if (K == 3) {
     if (CHK == 128)
       wide ? launch_small_conv_cfg<64, 3, 128, 16>(a, grid, s) : launch_small_conv_cfg<32, 3, 128, 16>(a, grid, s);
