@@ -127,6 +127,50 @@ __global__ __launch_bounds__(256) void groupnorm_rows_act_kernel(const float* x,
   }
 }
 
+// The same GroupNorm for rows of at most 256 * NPT values, held in registers
+// (thread t keeps elements t + 256 j): one read and one write pass instead of
+// three reads.  Every thread sums its elements in the same order as
+// groupnorm_rows_act_kernel, with the same operations.
+template <int NPT>
+__global__ __launch_bounds__(256) void groupnorm_rows_act_reg_kernel(const float* x, const float* g, const float* b,
+                                                                     float* out, int C, int L, float eps, int act) {
+  __shared__ double sh[256 / 64];
+  const long long row = blockIdx.x;
+  const int c = (int)(row % C);
+  const int tid = threadIdx.x;
+  // element tid + 256 j through a resource over [256 j, L) of the row, so
+  // the per-element offset is the one register 4 * tid and the range check
+  // zeroes (and drops) everything past L
+  auto part = [&](const float* base, int j) {
+    return uniform_rsrc(base + row * L + 256 * j, 4u * (unsigned)max(L - 256 * j, 0));
+  };
+  float v[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+    v[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(part(x, j), 4u * (unsigned)tid, 0, 0));
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+    if (tid + 256 * j < L) s += v[j];
+  const float mean = (float)(block_sum_d(s, sh) / (double)L);
+  double q = 0.0;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+    if (tid + 256 * j < L) {
+      const float d = v[j] - mean;
+      q += (double)d * d;
+    }
+  const float var = (float)(block_sum_d(q, sh) / (double)L);
+  const float den = sqrtf(var + eps);
+  const float gc = g[c], bc = b[c];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    float y = (v[j] - mean) / den * gc + bc;
+    if (act == ACT_GELU) y = gelu_as(y);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, y), part(out, j), 4u * (unsigned)tid, 0, 0);
+  }
+}
+
 // GroupNorm of the op-level ABI: x is [G][Cpg*S] (G groups, Cpg channels of
 // S elements each); every row is standardised over its Cpg*S values and
 // element i of row g gets the affine of channel g*Cpg + i/S
@@ -269,6 +313,12 @@ void launch_layernorm_cols(const float* x, const float* g, const float* b, float
 void launch_groupnorm_rows_act(const float* x, const float* g, const float* b, float* out, int B, int C, long long L,
                                float eps, int act, hipStream_t s) {
   if (B <= 0 || C <= 0 || L <= 0) return;
+  if (L <= 256 * 128) {
+    hipLaunchKernelGGL(groupnorm_rows_act_reg_kernel<128>, dim3((unsigned)((long long)B * C)), dim3(256), 0, s, x, g,
+                       b, out, C, (int)L, eps, act);
+    check_launch("groupnorm_rows_act");
+    return;
+  }
   hipLaunchKernelGGL(groupnorm_rows_act_kernel, dim3((unsigned)((long long)B * C)), dim3(256), 0, s, x, g, b, out, C,
                      L, eps, act);
   check_launch("groupnorm_rows_act");
