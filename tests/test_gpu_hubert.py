@@ -90,6 +90,22 @@ def test_config3_full_size_vs_oracle(sd, hub):
     assert np.abs(got - want).max() < 1e-3
 
 
+def test_long_input_feature_extractor_vs_oracle(sd, hub):
+    """12 s of input: the first conv's rows (37 999 samples) are longer than
+    the register-resident GroupNorm takes (32 768), so its three-pass kernel
+    runs; the feature extractor's output against the oracle's."""
+    x = syn.make_hubert_input(192000, seed=9)
+    hub.set_debug(True)
+    v2 = hub.encode(x, version=2)
+    hub.set_debug(False)
+    L = v2.shape[1]
+    assert L == 599
+    feats = hub.read("feats", (1, 512, L)).transpose(0, 2, 1)
+    want = H.HubertRef(sd).feature_extractor(x)
+    assert want.shape == feats.shape
+    assert rel_l2(feats, want) < TOL
+
+
 def test_full_size_batch_equals_per_chunk(hub):
     """Two 10 s chunks (499 frames: key-split attention) as a batch of 2
     equal the chunks encoded one by one, bit for bit."""
