@@ -62,6 +62,8 @@ def test_conv1d_small_vs_loops(ops, B, C, O, T, K, pl, pr, d):
     (1, 192, 96, 1000),    # flow post (C_out not a multiple of 64)
     (1, 256, 48, 300),     # widest staged reduction, C_out not a multiple of 32
     (1, 24, 40, 4097),     # narrow reduction, one column past a tile edge
+    (2, 256, 320, 4000),   # widest reduction on 64-column tiles (the largest LDS)
+    (1, 40, 64, 2001),     # reduction rows and staging passes not whole batches
 ])
 def test_conv1d_1x1_small_gemm(ops, B, C, O, T):
     """Plain 1x1 convs at a few thousand columns run the whole-reduction LDS
