@@ -98,11 +98,21 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
   const int kt_end = min(ntile, (ks + 1) * per);
   const bool slice_near = nb > 0 && kt_begin * 32 <= t0 + 31 + window && kt_end * 32 - 1 >= t0 - window;
 
-  // stage qs[d][t] = q[d][t0 + t] / sqrt(D)
-  for (int e = tid; e < Lds::Q; e += 256) {
-    const int d = e >> 5, j = e & 31;
-    const unsigned off = (d < D && t0 + j < P) ? 4u * (unsigned)(d * P + t0 + j) : kBufOut;
-    Qs[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(qrs, off, 0, 0)) / sq;
+  // stage qs[d][t] = q[d][t0 + t] / sqrt(D): every load in flight before
+  // the first division (a rolled loop waits out one round trip per element)
+  {
+    constexpr int QPT = Lds::Q / 256;
+    static_assert(Lds::Q % 256 == 0, "whole staging rounds");
+    float qv[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int e = tid + 256 * i;
+      const int d = e >> 5, j = e & 31;
+      const unsigned off = (d < D && t0 + j < P) ? 4u * (unsigned)(d * P + t0 + j) : kBufOut;
+      qv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(qrs, off, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) Qs[tid + 256 * i] = qv[i] / sq;
   }
   // band probabilities per wave: rows [0, nb) live, row nb takes the masked
   // lanes' (zero) updates so every lane can store unconditionally
