@@ -240,8 +240,19 @@ __global__ __launch_bounds__(256) void conv2d_reduce_kernel(Conv2dLaunch a) {
   const int z = (int)(idx / (npix * a.C_out));
   const int gi = z / a.B;
   const int bb = z - gi * a.B;
+  // the splits' partial sums in split order, kU loads in flight together
+  constexpr int kU = 8;
+  const long long kstride = (long long)nz * a.C_out * npix;
+  const float* pp = a.part + ((long long)z * a.C_out + co) * npix + p;
   float s = 0.f;
-  for (int k = 0; k < a.ksplit; ++k) s += a.part[((long long)(k * nz + z) * a.C_out + co) * npix + p];
+  for (int k0 = 0; k0 < a.ksplit; k0 += kU) {
+    float v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) v[u] = pp[min(k0 + u, a.ksplit - 1) * kstride];  // past ksplit: skipped below
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (k0 + u < a.ksplit) s += v[u];
+  }
   const int pa = (int)(p / a.OW);
   const int pw = (int)(p - (long long)pa * a.OW);
   const Conv2dGroup& G = a.g[gi];
