@@ -236,17 +236,34 @@ __global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv,
     }
   }
 
-  // band contribution: O^T[d][t] += sum_r emb_v[r][d] Pb[r][t]
+  // band contribution: O^T[d][t] += sum_r emb_v[r][d] Pb[r][t].  emb_v
+  // ([nb][D], nb * D < Lds::Q) goes through LDS, into the query tile's
+  // region once every wave has left the key loop, with all its loads in
+  // flight; a wave that saw the band lies in a slice that meets it.
+  if (slice_near) {  // uniform for the workgroup
+    __syncthreads();  // the query tile is dead
+    constexpr int QPT = Lds::Q / 256;
+    const int nv = nb * D;
+    const __amdgpu_buffer_rsrc_t ers = uniform_rsrc(emb_v, 4u * (unsigned)nv);
+    float ev[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int e = tid + 256 * i;
+      ev[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ers, e < nv ? 4u * (unsigned)e : kBufOut, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; ++i)
+      if (tid + 256 * i < nv) Qs[tid + 256 * i] = ev[i];
+    __syncthreads();
+  }
   if (band_seen) {
-    const __amdgpu_buffer_rsrc_t ers = uniform_rsrc(emb_v, 4u * (unsigned)(nb * D));
     for (int kk = 0; kk < (nb + 1) / 2; ++kk) {
       const int rr = 2 * kk + half;
       const float bval = Pb[rr * 32 + l32];  // row nb (odd nb) stays zero
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int d = dt * 32 + l32;
-        const unsigned off = (rr < nb && d < D) ? 4u * (unsigned)(rr * D + d) : kBufOut;
-        const float a = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ers, off, 0, 0));
+        const float a = (rr < nb && d < D) ? Qs[rr * D + d] : 0.f;
         O[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bval, O[dt], 0, 0, 0);
       }
     }
