@@ -59,8 +59,11 @@ struct AttnLds {
   static size_t bytes(int nb) { return sizeof(float) * (Q + VM + R + AWAVES * (nb + 1) * 32); }
 };
 
+// DT <= 2 (HuBERT's 64-wide heads) is held to three waves per SIMD (at most
+// 168 registers): three workgroups per CU, which sets the key split (4 at
+// 499 frames, 16.2 us per layer, against 3 splits and 21 us at two per CU).
 template <int DT>
-__global__ __launch_bounds__(256) void relpos_attention_kernel(const float* qkv, const float* emb_k,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT <= 2 ? 3 : 1))) void relpos_attention_kernel(const float* qkv, const float* emb_k,
                                                                const float* emb_v, float* out, float* part, int H,
                                                                int D, int P, int window, int KS) {
   using Lds = AttnLds<DT>;
