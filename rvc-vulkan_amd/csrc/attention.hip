@@ -439,7 +439,7 @@ size_t relpos_attention_scratch_floats(int B, int H, int D, int P, int window, b
 size_t relpos_attention_max_frames() { return (size_t)1 << 30; }
 
 void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out, float* scratch,
-                             int B, int H, int D, int P, int window, hipStream_t s) {
+                             size_t scratch_floats, int B, int H, int D, int P, int window, hipStream_t s) {
   RVC_CHECK(D >= 1 && D <= 128, "relpos_attention: head dim must be in [1,128]");
   RVC_CHECK(window >= 0 && window <= kMaxWindow, "relpos_attention: window must be in [0,15]");
   RVC_CHECK((emb_k == nullptr) == (emb_v == nullptr), "relpos_attention: emb_k and emb_v go together");
@@ -450,6 +450,9 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
             "relpos_attention: sequence too long for 32-bit offsets");
   const int KS = relpos_attention_splits(H, D, P, window, emb_k != nullptr);
   RVC_CHECK(KS == 1 || scratch != nullptr, "relpos_attention: scratch buffer required");
+  // the split partials fill B*H*KS*(D+2)*P floats of scratch
+  RVC_CHECK(KS == 1 || scratch_floats >= (size_t)B * H * KS * (D + 2) * P,
+            "relpos_attention: scratch buffer smaller than the key split's partial sums");
   const int dt = (D + 31) / 32;
   if (dt == 1) launch_dt<1>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
   else if (dt == 2) launch_dt<2>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);

@@ -1359,6 +1359,9 @@ void launch_small_conv_cfg(const ConvLaunch& a, dim3 grid, hipStream_t s) {
   constexpr size_t lds_red = sizeof(float) * NW * (BN / 32) * 16 * 64;  // the epilogue's partial tiles
   constexpr size_t lds = lds_stage > lds_red ? lds_stage : lds_red;
   static_assert(lds <= 160 * 1024, "staging LDS above the CU's 160 KiB");
+  // the gate epilogue pairs tile rows k and k + KO / 2 of one thread
+  RVC_CHECK(a.post != POST_WN_GATE || 32 * BN / (64 * NW) >= 2,
+            "conv_small: the WaveNet gate needs at least two tile rows per thread");
   if (lds > 65536) {
     static bool attr = false;  // per instantiation
     if (!attr) {
@@ -1385,8 +1388,10 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 320;
   const int BN = wide ? 64 : 32;
   // 128-channel chunks for the long 3-tap reductions (enc_p's FFN output
-  // conv, C_in = 768): half the chunk round trips
-  const int CHK = K == 3 && a.C_in % 128 == 0 && a.C_in >= 512 ? 128 : 64;
+  // conv, C_in = 768): half the chunk round trips.  Never for a gated launch:
+  // those run on sixteen waves, whose 32-column epilogue gives each thread a
+  // single tile row, and the gate pairs rows k and k + KO / 2 of one thread.
+  const int CHK = K == 3 && a.C_in % 128 == 0 && a.C_in >= 512 && !gate ? 128 : 64;
   const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
   // Waves per workgroup (each taking its share of every chunk's channels):
   // sixteen for the 128-channel 3-tap chunks (enc_p's FFN output conv, 768 x

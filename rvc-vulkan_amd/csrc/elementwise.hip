@@ -238,37 +238,76 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* W, const float* 
 }
 
 // ---- NSF sine source (runtime/models/vits.py:1468-1501) ----
-// Phase offsets: acc[p] = fmod(cumsum_{q<=p} rad2[q], 1) where
-// rad2[q] = fmod(f0[q]/sr*upp + 0.5, 1) - 0.5.  The cumulative sum is a
-// sequential float32 recurrence (numpy's cumsum order): after the workgroup
-// has staged rad2 in LDS, one thread runs the additions alone and the fmod
-// of every prefix is taken in parallel afterwards.
 // Per-frame phase of the NSF source.  rad_acc[p] = fmod(sum_{q<=p} r2[q], 1)
 // with r2[q] = fmod(f0[q]/sr*upp + 0.5, 1) - 0.5, the sum taken sequentially
-// in float32 (numpy's cumsum order), is the reference's _phase_offsets.
-// out[p + shift] = rad_acc[p]: shift 0 writes rad_acc itself; shift 1 writes
-// the offset each frame's phase adds (0 for frame 0, rad_acc[p-1] after it),
-// the form the har kernel reads.
+// in float32 (numpy's cumsum order, vits.py:1482-1488), is the reference's
+// _phase_offsets (:2404-2414).  out[p + shift] = rad_acc[p]: shift 0 writes
+// rad_acc itself; shift 1 writes the offset each frame's phase adds (0 for
+// frame 0, rad_acc[p-1] after it), the form the har kernel reads.
+//
+// Any P: the frames go through LDS in blocks of kPhaseBlock.  For each block
+// the workgroup forms r2 in parallel, one thread continues the running sum
+// over the block (the same sequential additions, carried from the previous
+// block in a register), and the fmod of every prefix is taken and stored in
+// parallel.  The serial thread reads its operands 16 at a time as float4s
+// and writes the prefixes back the same way, so the dependent chain is the
+// float additions themselves, not one LDS round trip per frame.
+constexpr int kPhaseBlock = 4096;
+
 __global__ __launch_bounds__(256) void sine_phase_kernel(const float* f0, float* out, int P, int upp,
                                                          float sr, int shift) {
-  extern __shared__ float r2[];
+  __shared__ float4 r4[kPhaseBlock / 4];
+  float* r2 = reinterpret_cast<float*>(r4);
   const int b = blockIdx.x;
   const float* fb = f0 + (long long)b * P;
-  for (int p = threadIdx.x; p < P; p += blockDim.x) {
-    const float rl = (fb[p] / sr) * (float)upp;
-    r2[p] = fmodf(rl + 0.5f, 1.0f) - 0.5f;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float c = r2[0];
-    for (int p = 1; p < P; ++p) {
-      c = c + r2[p];
-      r2[p] = c;
-    }
-  }
-  __syncthreads();
   float* ob = out + (long long)b * P;
-  for (int p = threadIdx.x; p + shift < P; p += blockDim.x) ob[p + shift] = fmodf(r2[p], 1.0f);
+  float c = 0.f;  // running sum (thread 0)
+  for (int p0 = 0; p0 < P; p0 += kPhaseBlock) {
+    const int n = min(kPhaseBlock, P - p0);
+    for (int p = threadIdx.x; p < kPhaseBlock; p += blockDim.x) {
+      float v = 0.f;  // the block's tail past P stays 0 and is never stored
+      if (p < n) {
+        const float rl = (fb[p0 + p] / sr) * (float)upp;
+        v = fmodf(rl + 0.5f, 1.0f) - 0.5f;
+      }
+      r2[p] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      // frame 0 starts the sum with r2[0] itself, as numpy's cumsum does
+      for (int q = 0; q < (n + 15) / 16; ++q) {
+        float4 a = r4[4 * q], bq = r4[4 * q + 1], cq = r4[4 * q + 2], dq = r4[4 * q + 3];
+        if (p0 == 0 && q == 0) {
+          c = a.x;
+        } else {
+          c = c + a.x;
+        }
+        a.x = c;
+        c = c + a.y; a.y = c;
+        c = c + a.z; a.z = c;
+        c = c + a.w; a.w = c;
+        c = c + bq.x; bq.x = c;
+        c = c + bq.y; bq.y = c;
+        c = c + bq.z; bq.z = c;
+        c = c + bq.w; bq.w = c;
+        c = c + cq.x; cq.x = c;
+        c = c + cq.y; cq.y = c;
+        c = c + cq.z; cq.z = c;
+        c = c + cq.w; cq.w = c;
+        c = c + dq.x; dq.x = c;
+        c = c + dq.y; dq.y = c;
+        c = c + dq.z; dq.z = c;
+        c = c + dq.w; dq.w = c;
+        r4[4 * q] = a; r4[4 * q + 1] = bq; r4[4 * q + 2] = cq; r4[4 * q + 3] = dq;
+      }
+      // c carries into the next block; only the last block can be partial,
+      // so the padding zeros it adds are never carried
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < n; p += blockDim.x)
+      if (p0 + p + shift < P) ob[p0 + p + shift] = fmodf(r2[p], 1.0f);
+    __syncthreads();  // r2 is refilled by the next block
+  }
   if (shift && threadIdx.x == 0) ob[0] = 0.f;
 }
 
@@ -438,8 +477,7 @@ void launch_gemv(const float* W, const float* bias, const float* g, long long gb
 }
 void launch_sine_phase(const float* f0, float* out, int B, int P, int upp, float sr, int shift, hipStream_t s) {
   if ((long long)B * P == 0) return;
-  RVC_CHECK((size_t)P * sizeof(float) <= 65536, "sine_source: too many frames per chunk (max 16384)");
-  hipLaunchKernelGGL(sine_phase_kernel, dim3(B), dim3(256), P * sizeof(float), s, f0, out, P, upp, sr, shift);
+  hipLaunchKernelGGL(sine_phase_kernel, dim3(B), dim3(256), 0, s, f0, out, P, upp, sr, shift);
   check_launch("sine_phase");
 }
 void launch_sine_source(const float* f0, const float* ns, float* har, float* off, const float* seg_off, int B, int P,

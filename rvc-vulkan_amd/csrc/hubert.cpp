@@ -274,7 +274,8 @@ struct Hubert : SessionBase {
     float* ff = buf("ffn", (size_t)B * F * L);
     float* xa = buf("xa", (size_t)B * HL);
     float* xb_ = buf("xb", (size_t)B * HL);
-    float* part = buf("attn_part", std::max<size_t>(1, relpos_attention_scratch_floats(B, kHeads, D, (int)L, 0, false)));
+    const size_t part_n = std::max<size_t>(1, relpos_attention_scratch_floats(B, kHeads, D, (int)L, 0, false));
+    float* part = buf("attn_part", part_n);
     const float* cur = x0;
     const int nl = version == 1 ? 9 : n_layers;
     for (int i = 0; i < nl; ++i) {
@@ -282,7 +283,7 @@ struct Hubert : SessionBase {
       float* xo = (i & 1) ? xb_ : xa;
       conv("hub.qkv", c1x1(cur, HL, Ly.wqkv, Ly.bqkv, qkv, B, H, 3 * H, (int)L));
       run("hub.attn", 4.0 * B * kHeads * (double)L * L * D, 4.0 * B * 4.0 * HL,
-          [&] { launch_relpos_attention(qkv, nullptr, nullptr, att, part, B, kHeads, D, (int)L, 0, s); });
+          [&] { launch_relpos_attention(qkv, nullptr, nullptr, att, part, part_n, B, kHeads, D, (int)L, 0, s); });
       ConvLaunch co = c1x1(att, HL, Ly.wo, Ly.bo, t1, B, H, H, (int)L);
       co.g[0].res = cur; co.rb = HL; co.rc = L;
       conv("hub.o", co);

@@ -382,10 +382,12 @@ void launch_rmsnorm_rows(const float* x, const float* g, float* out, long long r
 // Windowed relative-position attention, all heads (emb_k = emb_v = null:
 // plain attention).
 // qkv[b][3*H*D][P] (q, k, v stacked), emb_k/emb_v [2w+1][D], out[b][H*D][P];
-// scratch holds relpos_attention_scratch_floats(B,H,D,P,window,band) floats
-// (band: emb_k given; may be null when that is 0).
+// scratch (scratch_floats floats) must hold
+// relpos_attention_scratch_floats(B,H,D,P,window,band) floats (band: emb_k
+// given; may be null when that is 0); a smaller buffer is an error.
 void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out,
-                             float* scratch, int B, int H, int D, int P, int window, hipStream_t s);
+                             float* scratch, size_t scratch_floats, int B, int H, int D, int P, int window,
+                             hipStream_t s);
 size_t relpos_attention_scratch_floats(int B, int H, int D, int P, int window, bool band);
 size_t relpos_attention_max_frames();
 

@@ -415,13 +415,14 @@ struct Synth : SessionBase {
     float* att = buf("att", (size_t)B * HP);
     float* o = buf("enco", (size_t)B * HP);
     float* f = buf("ffn", (size_t)B * F * P);
-    float* apart = buf("attn_part", std::max<size_t>(1, relpos_attention_scratch_floats(B, heads, kc, P, kWindow, true)));
+    const size_t apart_n = std::max<size_t>(1, relpos_attention_scratch_floats(B, heads, kc, P, kWindow, true));
+    float* apart = buf("attn_part", apart_n);
     const float* x = xin;
     for (int i = 0; i < n_layers; ++i) {
       const EncL& L = enc[i];
       conv("enc.qkv", with16(c1x1(x, HP, L.wqkv, L.bqkv, qkv, B, H, 3 * H, P), L.wqkv16));
       run("enc.attn", 4.0 * B * heads * (double)P * P * kc, 4.0 * B * 4 * HP,
-          [&] { launch_relpos_attention(qkv, L.ek, L.ev, att, apart, B, heads, kc, P, kWindow, s); });
+          [&] { launch_relpos_attention(qkv, L.ek, L.ev, att, apart, apart_n, B, heads, kc, P, kWindow, s); });
       ConvLaunch co = with16(c1x1(att, HP, L.wo, L.bo, o, B, H, H, P), L.wo16);
       co.g[0].res = x; co.rb = HP; co.rc = P;
       conv("enc.o", co);

@@ -65,7 +65,6 @@ class VitsConfig:
         self.gin_channels = int(w["emb_g.weight"].shape[1])
 
     def __repr__(self):
-        return (f"VitsConfig(phone={self.phone_dim}, hidden={self.hidden}, filter={self.filter}, "
-                f"heads={self.n_heads}, layers={self.n_layers}, n_ups={self.n_ups}, "
-                f"rates={self.upsample_rates}, kernels={self.upsample_kernels}, n_spk={self.n_spk}, "
-                f"gin={self.gin_channels}, sr={self.sr})")
+        fields = ("sr", "phone_dim", "hidden", "filter", "n_heads", "n_layers", "n_spk", "gin_channels",
+                  "upsample_rates", "upsample_kernels")
+        return "VitsConfig<" + " ".join(f"{k}:{getattr(self, k)}" for k in fields) + ">"

@@ -18,6 +18,13 @@ One deliberate difference: there is no host shortcut for small tensors (the
 reference computes < 1024-element inputs with numpy, ``runtime/vulkan_ops.py
 :115``).  Every call here runs on the GPU, so results never silently come
 from a CPU path.
+
+Observability as in the reference: ``stats_reset()`` / ``stats_snapshot()``
+count host->device uploads and device->host downloads with their bytes
+(``runtime/vulkan_ops.py:139-150, 225-249``; every upload of an op argument,
+``persistent_upload`` and ``PersistentBuffer.update`` counts, as does every
+result download), and ``RVC_PROFILE=1`` times each module-level op into the
+table of ``rvc_hip.profiler`` under ``"<op>/gpu"``.
 """
 
 from __future__ import annotations
@@ -28,8 +35,11 @@ import threading
 import numpy as np
 
 from . import _hip
+from . import profiler
 
 __all__ = [
+    "stats_reset",
+    "stats_snapshot",
     "HipContext",
     "PersistentBuffer",
     "get_context",
@@ -49,6 +59,50 @@ __all__ = [
 ]
 
 _F32P = ctypes.POINTER(ctypes.c_float)
+
+# ------------------------------------------------------------------ transfer counters
+_stats_lock = threading.Lock()
+_stats = {"uploads": 0, "downloads": 0, "upload_bytes": 0, "download_bytes": 0}
+
+
+def stats_reset() -> None:
+    """Zero the upload / download counters."""
+    with _stats_lock:
+        for k in _stats:
+            _stats[k] = 0
+
+
+def stats_snapshot() -> dict:
+    """{"uploads", "downloads", "upload_bytes", "download_bytes"} since the
+    last reset (process-wide, every context)."""
+    with _stats_lock:
+        return dict(_stats)
+
+
+def _count(kind: str, nbytes: int) -> None:
+    with _stats_lock:
+        _stats[kind + "s"] += 1
+        _stats[kind + "_bytes"] += int(nbytes)
+
+
+def _traced(name: str):
+    """Time the wrapped op under ``name`` when ``RVC_PROFILE`` is on (the
+    reference's ``traced``, ``runtime/vulkan_ops.py:35-48``)."""
+
+    def deco(fn):
+        def wrap(*args, **kwargs):
+            if not profiler.enabled():
+                return fn(*args, **kwargs)
+            with profiler.profile_op(name):
+                return fn(*args, **kwargs)
+
+        wrap.__name__ = fn.__name__
+        wrap.__qualname__ = fn.__qualname__
+        wrap.__doc__ = fn.__doc__
+        wrap.__wrapped__ = fn
+        return wrap
+
+    return deco
 
 
 def _f32_bits(v: float) -> int:
@@ -110,8 +164,9 @@ class PersistentBuffer:
             raise RuntimeError("PersistentBuffer already freed")
         if a.size * 4 > self.nbytes:
             raise ValueError(f"PersistentBuffer.update: {a.size * 4} bytes > {self.nbytes}")
-        _hip._check(_hip.get_lib().rvc_mem_upload_to(self._ctx.handle, a.ctypes.data_as(_F32P), a.size,
-                                                      self._buf), "rvc_mem_upload_to")
+        _count("upload", a.nbytes)
+        _hip._check(self._ctx._lib.rvc_mem_upload_to(self._ctx.handle, a.ctypes.data_as(_F32P), a.size,
+                                                     self._buf), "rvc_mem_upload_to")
 
     def __del__(self):
         try:
@@ -145,6 +200,7 @@ class HipContext:
     def upload(self, a) -> int:
         a = np.ascontiguousarray(a)
         out = ctypes.c_int64(0)
+        _count("upload", a.nbytes)
         with self._lock:
             _hip._check(self._lib.rvc_mem_upload_bytes(self.handle, a.ctypes.data_as(ctypes.c_void_p),
                                                        a.nbytes, ctypes.byref(out)), "rvc_mem_upload_bytes")
@@ -163,6 +219,7 @@ class HipContext:
 
     def download(self, buf: int, shape, dtype=np.float32) -> np.ndarray:
         out = np.empty(shape, dtype=dtype)
+        _count("download", out.nbytes)
         with self._lock:
             _hip._check(self._lib.rvc_mem_download_bytes(self.handle, int(buf), out.ctypes.data_as(ctypes.c_void_p),
                                                          out.nbytes), "rvc_mem_download_bytes")
@@ -472,55 +529,68 @@ def get_context() -> HipContext:
 
 
 # ------------------------------------------------------------------ module-level ops
+@_traced("matmul/gpu")
 def matmul(a, b, buf_a=None, buf_b=None):
     return get_context().matmul(a, b, buf_a=buf_a, buf_b=buf_b)
 
 
+@_traced("add/gpu")
 def add(a, b, buf_a=None, buf_b=None):
     return get_context().add(a, b, buf_a=buf_a, buf_b=buf_b)
 
 
+@_traced("mul/gpu")
 def mul(a, b, buf_a=None, buf_b=None):
     return get_context().mul(a, b, buf_a=buf_a, buf_b=buf_b)
 
 
+@_traced("relu/gpu")
 def relu(a, buf_a=None):
     return get_context().relu(a, buf_a=buf_a)
 
 
+@_traced("leaky_relu/gpu")
 def leaky_relu(a, negative_slope=0.1):
     return get_context().leaky_relu(a, negative_slope)
 
 
+@_traced("conv1d/gpu")
 def conv1d(x, w, b=None, stride=1, padding=0, dilation=1, buf_w=None, buf_b=None):
     return get_context().conv1d(x, w, b, stride, padding, dilation, buf_w=buf_w, buf_b=buf_b)
 
 
+@_traced("conv_transpose1d/gpu")
 def conv_transpose1d(x, w, b=None, stride=1, padding=0, output_padding=0, dilation=1, buf_w=None,
                      buf_b=None):
     return get_context().conv_transpose1d(x, w, b, stride, padding, output_padding, dilation,
                                           buf_w=buf_w, buf_b=buf_b)
 
 
+@_traced("embedding/gpu")
 def embedding(ids, table, buf_table=None):
     return get_context().embedding(ids, table, buf_table=buf_table)
 
 
+@_traced("add_inplace/gpu")
 def add_inplace(a, b, buf_a=None, buf_b=None):
     return get_context().add_inplace(a, b, buf_a=buf_a, buf_b=buf_b)
 
 
+@_traced("mul_inplace/gpu")
 def mul_inplace(a, b, buf_a=None, buf_b=None):
     return get_context().mul_inplace(a, b, buf_a=buf_a, buf_b=buf_b)
 
 
+@_traced("layer_norm/gpu")
 def layer_norm(x, gamma, beta, eps=1e-5, buf_gamma=None, buf_beta=None):
     return get_context().layer_norm(x, gamma, beta, eps, buf_gamma=buf_gamma, buf_beta=buf_beta)
 
 
+@_traced("rmsnorm/gpu")
 def rmsnorm(x, gamma, eps=1e-5, buf_gamma=None):
     return get_context().rmsnorm(x, gamma, eps, buf_gamma=buf_gamma)
 
 
+@_traced("softmax/gpu")
 def softmax(x):
     return get_context().softmax(x)

@@ -72,6 +72,29 @@ def test_phase_offsets(gold, hip):
     np.testing.assert_allclose(got, gold["phase_offsets"], rtol=0, atol=1e-6)
 
 
+@pytest.mark.parametrize("P", [16383, 16384, 20000, 70001])
+def test_phase_offsets_long(hip, P):
+    """Past one LDS block of the scan (4096 frames) and past the old
+    16 384-frame cap: bit-for-bit against the oracle's float32 cumsum."""
+    rng = np.random.default_rng(P)
+    f0 = rng.uniform(80.0, 400.0, size=(1, P)).astype(np.float32)
+    f0[:, rng.random(P) < 0.2] = 0.0
+    got = hip.phase_offsets(f0)
+    want = V.Synthesizer.phase_offsets(hip_oracle_stub(hip), f0)
+    assert got.shape == want.shape
+    np.testing.assert_array_equal(got, want)
+
+
+def hip_oracle_stub(hip):
+    """The oracle's phase_offsets needs only cfg.sr and cfg.upp."""
+    class _S:
+        pass
+
+    s = _S()
+    s.cfg = hip.cfg
+    return s
+
+
 @pytest.mark.parametrize("i", [0, 1, 2])
 def test_partial_prep_and_infer(gold, hip, i):
     head, length = (int(v) for v in gold["parts"][i])
