@@ -269,6 +269,21 @@ int32_t rvc_synth_finalize(int64_t s, int64_t sr, const int64_t* rates, const in
 int32_t rvc_synth_infer(int64_t s, const float* phone, const int64_t* pitch, const float* nsff0,
                         const int64_t* sid, const float* nz, const float* ns, int64_t B, int64_t P,
                         float* wave);
+/* Deferred form of rvc_synth_infer (SynthesizerTrn.infer(..., phone_gpu=...,
+ * _defer=True), runtime/models/vits.py:2352-2402, 2551-2595, used by
+ * Pipeline's chunk overlap, runtime/pipeline.py:1010-1080): queue the whole
+ * synthesis and the waveform's copy into pinned staging, return a ticket
+ * (> 0) without waiting, -1 on error.  phone is a host [B,P,phone_dim] array,
+ * or 0 with phone_buf the engine buffer holding it (the resident phone_gpu);
+ * exactly one of them.  Host arrays may be reused once the call returns.
+ * At most 8 calls are outstanding per session; each is ended by
+ * rvc_synth_collect (waits, copies the wave [B,P*upp] out) or
+ * rvc_synth_abort (waits, drops it).  Calls run in submission order. */
+int64_t rvc_synth_submit(int64_t s, const float* phone, int64_t phone_buf, const int64_t* pitch,
+                         const float* nsff0, const int64_t* sid, const float* nz, const float* ns, int64_t B,
+                         int64_t P);
+int32_t rvc_synth_collect(int64_t s, int64_t ticket, float* wave);
+int32_t rvc_synth_abort(int64_t s, int64_t ticket);
 /* Same with engine buffer ids (inputs already resident; pitch/sid hold int64).
  * A pitch or sid id outside [-rows, rows) fails the call (-1, "... out of
  * range"), as the host path and numpy's take do. */

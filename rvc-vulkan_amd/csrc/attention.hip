@@ -438,8 +438,9 @@ size_t relpos_attention_scratch_floats(int B, int H, int D, int P, int window, b
 
 size_t relpos_attention_max_frames() { return (size_t)1 << 30; }
 
-void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out, float* scratch,
-                             size_t scratch_floats, int B, int H, int D, int P, int window, hipStream_t s) {
+int launch_relpos_attention_partials(const float* qkv, const float* emb_k, const float* emb_v, float* out,
+                                     float* scratch, size_t scratch_floats, int B, int H, int D, int P, int window,
+                                     hipStream_t s) {
   RVC_CHECK(D >= 1 && D <= 128, "relpos_attention: head dim must be in [1,128]");
   RVC_CHECK(window >= 0 && window <= kMaxWindow, "relpos_attention: window must be in [0,15]");
   RVC_CHECK((emb_k == nullptr) == (emb_v == nullptr), "relpos_attention: emb_k and emb_v go together");
@@ -458,6 +459,13 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
   else if (dt == 2) launch_dt<2>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
   else if (dt == 3) launch_dt<3>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
   else launch_dt<4>(qkv, emb_k, emb_v, out, scratch, B, H, D, P, window, KS, s);
+  return KS;
+}
+
+void launch_relpos_attention(const float* qkv, const float* emb_k, const float* emb_v, float* out, float* scratch,
+                             size_t scratch_floats, int B, int H, int D, int P, int window, hipStream_t s) {
+  const int KS =
+      launch_relpos_attention_partials(qkv, emb_k, emb_v, out, scratch, scratch_floats, B, H, D, P, window, s);
   if (KS > 1) {
     const long long n = (long long)B * H * D * P;
     hipLaunchKernelGGL(relpos_attention_merge, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, scratch, out, H, D,

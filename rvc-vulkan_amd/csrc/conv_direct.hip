@@ -125,6 +125,118 @@ __global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
   *o = v;
 }
 
+// The decoder's conv_post (C_out = 1, stride 1, dilation 1, odd K <= 9 with
+// "same" padding), HBM-bound: it streams every input channel once (with x2 /
+// x3 the three ResBlock outputs of the last stage, averaged while staged).
+// A workgroup owns kPostTile outputs, thread t outputs t0 + 4t .. + 3.  The
+// channels go through LDS in groups of kPostCh: for each group every thread
+// loads one aligned float4 of each channel row of each input (the first two
+// threads also the 8-sample halo), forms ((x + x2) + x3) / 3 and the input
+// activation, and stores the float4 to the group's LDS window
+// [kPostCh][kPostTile + 8] (window column 0 = sample t0 - 4).  The next
+// group's loads are issued before the current group's taps are summed, and
+// the window is double-buffered, so one barrier per group remains.  Per
+// output the sum runs channel-major, taps inner, like conv1d_rows_kernel.
+// Requirements (checked by the launcher): L % 4 == 0 and 16-byte aligned
+// rows, so each aligned float4 lies wholly inside [0, L) or wholly outside,
+// and outside ones read 0 through the buffer range.
+constexpr int kPostTile = 1024, kPostCh = 4, kPostW = kPostTile + 8;
+template <int K>
+__global__ __launch_bounds__(256) void conv_post_kernel(DirectConvArgs a) {
+  __shared__ float4 win[2][kPostCh][kPostW / 4];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.y;
+  const int t0 = blockIdx.x * kPostTile;
+  const int nin = a.x2 ? 3 : 1;
+  const unsigned range = 4u * (unsigned)((a.C_in - 1) * (int)a.xc + a.L_in);
+  const __amdgpu_buffer_rsrc_t r0 = uniform_rsrc(a.x + (long long)b * a.xb, range);
+  const __amdgpu_buffer_rsrc_t r1 = uniform_rsrc(nin == 3 ? a.x2 + (long long)b * a.xb : a.x, range);
+  const __amdgpu_buffer_rsrc_t r2 = uniform_rsrc(nin == 3 ? a.x3 + (long long)b * a.xb : a.x, range);
+  // window float4 f covers samples t0 - 4 + 4f .. + 3: f = tid, and f = 256 + tid for tid < 2
+  auto foff = [&](int f, int c) -> unsigned {
+    const int t = t0 - 4 + 4 * f;
+    return (t >= 0 && t < a.L_in) ? 4u * (unsigned)(c * (int)a.xc + t) : kBufOut;
+  };
+  const bool halo = tid < 2;
+  float4 v[3][kPostCh], h[3][kPostCh];
+  auto load = [&](int c0) {
+#pragma unroll
+    for (int r = 0; r < kPostCh; ++r) {
+      const unsigned o = foff(tid, c0 + r);
+      const unsigned oh = halo ? foff(256 + tid, c0 + r) : kBufOut;
+      v[0][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r0, o, 0, 0));
+      if (halo) h[0][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r0, oh, 0, 0));
+      if (nin == 3) {
+        v[1][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r1, o, 0, 0));
+        v[2][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r2, o, 0, 0));
+        if (halo) {
+          h[1][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r1, oh, 0, 0));
+          h[2][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r2, oh, 0, 0));
+        }
+      }
+    }
+  };
+  auto prep = [&](float4 x, float4 y, float4 z) -> float4 {
+    float e[4] = {x.x, x.y, x.z, x.w};
+    if (nin == 3) {
+      const float f[4] = {y.x, y.y, y.z, y.w}, g[4] = {z.x, z.y, z.z, z.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e[i] = ((e[i] + f[i]) + g[i]) / 3.0f;  // the decoder's ((o1 + o2) + o3) / 3
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = act_in(e[i], a.in_act, a.in_slope);
+    return float4{e[0], e[1], e[2], e[3]};
+  };
+  constexpr int c_off = 4 - (K - 1) / 2;  // window column of output 4t's first tap, minus 4t
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int ng = a.C_in / kPostCh;
+  load(0);
+  for (int g = 0; g < ng; ++g) {
+    const int buf = g & 1;
+#pragma unroll
+    for (int r = 0; r < kPostCh; ++r) {
+      win[buf][r][tid] = prep(v[0][r], v[1][r], v[2][r]);
+      if (halo) win[buf][r][256 + tid] = prep(h[0][r], h[1][r], h[2][r]);
+    }
+    __syncthreads();
+    if (g + 1 < ng) load((g + 1) * kPostCh);
+#pragma unroll
+    for (int r = 0; r < kPostCh; ++r) {
+      const float* wl = reinterpret_cast<const float*>(&win[buf][r][0]) + 4 * tid + c_off;
+      float x[K + 3];
+#pragma unroll
+      for (int i = 0; i < K + 3; ++i) x[i] = wl[i];
+      const float* wr = a.w + (long long)(g * kPostCh + r) * K;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const float wv = wr[k];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] += wv * x[q + k];
+      }
+    }
+  }
+  const int o0 = t0 + 4 * tid;
+  if (o0 >= a.n_out) return;
+  float res[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float u = acc[q];
+    if (a.bias) u = u + a.bias[0];
+    res[q] = act_out(u, a.out_act, a.out_slope);
+  }
+  float* ob = a.out + (long long)b * a.ob + o0;
+  *reinterpret_cast<float4*>(ob) = float4{res[0], res[1], res[2], res[3]};
+}
+
+bool conv_post_ok(const DirectConvArgs& a) {
+  return a.C_out == 1 && a.stride == 1 && a.dil == 1 && a.K % 2 == 1 && a.K >= 3 && a.K <= 9 && a.in_off == -(a.K - 1) / 2 &&
+         a.n_out == a.L_in && a.L_in % 4 == 0 && a.C_in % kPostCh == 0 && a.xc % 4 == 0 && a.xb % 4 == 0 &&
+         a.ob % 4 == 0 && a.combine == COMB_STORE && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (!a.x2 || ((reinterpret_cast<uintptr_t>(a.x2) & 15) == 0 &&
+                                                            (reinterpret_cast<uintptr_t>(a.x3) & 15) == 0)) &&
+         4.0 * ((a.C_in - 1) * (double)a.xc + a.L_in) < 2147483648.0;
+}
+
 // Single-input-channel convolutions at dilation 1 (the NSF noise convs of
 // the decoder stages the ConvTranspose epilogue does not cover: 1 -> C with
 // k = 2 * stride, runtime/models/vits.py:1628-1635).  A workgroup owns
@@ -296,6 +408,14 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
   } else if (a.C_out >= 8) {
     dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);
     hipLaunchKernelGGL(conv1d_direct_kernel<8>, grid, dim3(256), 0, s, a);
+  } else if (conv_post_ok(a)) {
+    dim3 grid((a.n_out + kPostTile - 1) / kPostTile, a.B);
+    switch (a.K) {
+      case 3: hipLaunchKernelGGL(conv_post_kernel<3>, grid, dim3(256), 0, s, a); break;
+      case 5: hipLaunchKernelGGL(conv_post_kernel<5>, grid, dim3(256), 0, s, a); break;
+      case 7: hipLaunchKernelGGL(conv_post_kernel<7>, grid, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL(conv_post_kernel<9>, grid, dim3(256), 0, s, a); break;
+    }
   } else if (a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax) {
     dim3 grid((a.n_out + kRowOut - 1) / kRowOut, a.C_out, a.B);
     hipLaunchKernelGGL(conv1d_rows_kernel, grid, dim3(256), 0, s, a);

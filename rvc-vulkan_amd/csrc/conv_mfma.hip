@@ -924,6 +924,19 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
       wv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
     }
   }
+  // LayerNorm on the way in: gamma / beta go to LDS behind xs, with the
+  // column statistics (float64 partial sums [RS][BN], then mean and den)
+  const bool ln = a.ln_g != nullptr;
+  float* lng = xs + (n_it + LB - 1) / LB * LB * 256;
+  float* lnb = lng + 256;
+  double* lnp = reinterpret_cast<double*>(lnb + 256);
+  float* lnm = reinterpret_cast<float*>(lnp + 256);
+  float* lnd = lnm + BN;
+  float gv = 0.f, bv0 = 0.f;
+  if (ln && tid < C_in) {
+    gv = a.ln_g[tid];
+    bv0 = a.ln_b[tid];
+  }
   for (int j0 = 0; j0 < n_it; j0 += LB) {
     float v[LB];
     xload(j0, v);
@@ -931,10 +944,68 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (32 * j < C_in) reinterpret_cast<float4*>(ws)[tid + 256 * j] = wv[j];  // uniform
+      if (ln) {
+        lng[tid] = gv;
+        lnb[tid] = bv0;
+      }
     }
     xstore(j0, v);
   }
   __syncthreads();
+  if (ln) {
+    // thread (xrow, xcol) staged rows xrow + RS * j, j < n_it, of column xcol.
+    // Four float64 accumulators (n_it = C_in / RS is a multiple of 4 for
+    // C_in % 8 == 0 and RS <= 8 when C_in % 32 == 0; else the tail loop runs):
+    // float64 sums of float32 values this few are exact in any order.
+    double s4[4] = {0.0, 0.0, 0.0, 0.0};
+    int j = 0;
+    for (; j + 4 <= n_it; j += 4)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s4[u] += xs[(j + u) * 256 + tid];
+    for (; j < n_it; ++j) s4[0] += xs[j * 256 + tid];
+    lnp[tid] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    __syncthreads();
+    if (tid < BN) {
+      double t = 0.0;
+      for (int g = 0; g < RS; ++g) t += lnp[g * BN + tid];
+      lnm[tid] = (float)(t / C_in);
+    }
+    __syncthreads();
+    const float mu = lnm[xcol];
+    double q4[4] = {0.0, 0.0, 0.0, 0.0};
+    j = 0;
+    for (; j + 4 <= n_it; j += 4)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float d = xs[(j + u) * 256 + tid] - mu;
+        q4[u] += (double)d * d;
+      }
+    for (; j < n_it; ++j) {
+      const float d = xs[j * 256 + tid] - mu;
+      q4[0] += (double)d * d;
+    }
+    lnp[tid] = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+    __syncthreads();
+    if (tid < BN) {
+      double t = 0.0;
+      for (int g = 0; g < RS; ++g) t += lnp[g * BN + tid];
+      lnd[tid] = 1.0f / sqrtf((float)(t / C_in) + a.ln_eps);
+    }
+    __syncthreads();
+    // every C_out tile of the column block normalises the same staged tile,
+    // so the per-element division becomes a multiply by the column's 1 / den
+    const float rdn = lnd[xcol];
+    const bool wr = blockIdx.y == 0 && a.ln_out != nullptr && i0 + xcol < a.L_in;
+    float* lo = a.ln_out + (long long)b * a.ln_ob + i0 + xcol;
+#pragma unroll 4
+    for (int jj = 0; jj < n_it; ++jj) {
+      const int r = xrow + RS * jj;
+      const float y = (xs[jj * 256 + tid] - mu) * rdn * lng[r] + lnb[r];
+      xs[jj * 256 + tid] = y;
+      if (wr) lo[(long long)r * a.ln_oc] = y;
+    }
+    __syncthreads();
+  }
 
   floatx16 acc[TN];
 #pragma unroll
@@ -1428,9 +1499,15 @@ bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
   // ws: C_in rounded up to 32 rows of 32; xs: the staging passes rounded up
   // to the batch of 12, 256 floats each; the epilogue's four waves' tiles
   const size_t n_it = (size_t)a.C_in / (256 / BN);
-  const size_t lds = sizeof(float) * std::max(((size_t)a.C_in + 31) / 32 * 32 * 32 + (n_it + 11) / 12 * 12 * 256,
-                                              (size_t)4 * (BN / 32) * 1024);
-  constexpr int kMaxLds = sizeof(float) * (256 * 32 + 72 * 256);  // C_in = 256, BN = 64
+  // the LayerNorm's gamma / beta (256 each), float64 partials (256) and the
+  // mean / den columns (BN each) behind xs
+  const size_t ln_floats = a.ln_g ? 256 + 256 + 2 * 256 + 2 * 64 : 0;
+  const size_t lds =
+      sizeof(float) * std::max(((size_t)a.C_in + 31) / 32 * 32 * 32 + (n_it + 11) / 12 * 12 * 256 + ln_floats,
+                               (size_t)4 * (BN / 32) * 1024);
+  constexpr int kMaxLds = sizeof(float) * (256 * 32 + 72 * 256 + 1152);  // C_in = 256, BN = 64, LayerNorm
+  RVC_CHECK(!a.ln_g || (a.n_groups == 1 && a.in_act == ACT_NONE && a.ln_b),
+            "conv1x1_small: the staged LayerNorm takes one group, no input activation, gamma and beta");
   RVC_CHECK(lds <= (size_t)kMaxLds, "conv1x1_small: LDS above its limit");
   const dim3 grid((unsigned)((n_out + BN - 1) / BN), (unsigned)nco, (unsigned)z);
   static bool attr = false;
@@ -1540,6 +1617,8 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
     RVC_CHECK((reinterpret_cast<uintptr_t>(a.g[g].w) & 15) == 0, "conv1d_mfma: weights must be 16-byte aligned");
   }
   if (max_n_out(a) == 0) return;
+  RVC_CHECK(!a.ln_g || (step == 1 && small_gemm_ok(a)),
+            "conv1d_mfma: a staged LayerNorm needs the whole-reduction 1x1 kernel (C_in <= 256, <= 8192 columns)");
   if (step == 1 && small_gemm_ok(a) && launch_small_gemm(a, s)) return;
   if (step == 1 && small_conv_ok(a) && launch_small_conv(a, s)) return;
   for (int g = 0; g < a.n_groups; ++g)

@@ -158,6 +158,18 @@ struct ConvLaunch {
   // finish count, reset by the launch's last workgroup) for dynamic item
   // scheduling; null: static round-robin.  One launch at a time per buffer.
   unsigned* queue;
+  // LayerNorm of the input over its C_in channels, applied while it is
+  // staged (the whole-reduction 1x1 kernel, single group, no input
+  // activation): x' = (x - mean_t) * (1 / sqrt(var_t + ln_eps)) * ln_g[c] + ln_b[c]
+  // per column t (two-pass, float64 sums, the formulas of the LayerNorm
+  // kernels).  The workgroups of C_out tile 0 also store x' to ln_out
+  // (batch / channel strides ln_ob / ln_oc), for the consumers of the
+  // normalised tensor itself.  ln_g == null: no LayerNorm.
+  const float* ln_g;
+  const float* ln_b;
+  float* ln_out;
+  long long ln_ob, ln_oc;
+  float ln_eps;
 };
 enum Post : int { POST_NONE = 0, POST_WN_GATE = 1, POST_WN_UPDATE = 2 };
 
@@ -390,6 +402,35 @@ void launch_relpos_attention(const float* qkv, const float* emb_k, const float* 
                              hipStream_t s);
 size_t relpos_attention_scratch_floats(int B, int H, int D, int P, int window, bool band);
 size_t relpos_attention_max_frames();
+// The key split the attention kernel uses for (H, D, P, window); a function
+// of the shape only, never of B.
+int relpos_attention_splits(int H, int D, int P, int window, bool band);
+// The attention kernel alone, without the merge launch: returns the key
+// split KS.  KS == 1: out holds the attention output; KS > 1: scratch holds
+// the partials part[b][h][ks] = (m[P], l[P], O[D][P]) for a consumer that
+// merges them (launch_attn_out_ln).
+int launch_relpos_attention_partials(const float* qkv, const float* emb_k, const float* emb_v, float* out,
+                                     float* scratch, size_t scratch_floats, int B, int H, int D, int P, int window,
+                                     hipStream_t s);
+
+// enc_p's attention output block in one launch (attn_out.hip): merge of the
+// attention partials (KS > 1) or the merged output (KS == 1), conv_o + bias,
+// + the residual, LayerNorm over the C = H * D channels.  Tensors [B][C][P]
+// contiguous; w packed [C_in][ld] (w[ci * ld + co]).
+struct AttnOutArgs {
+  const float* part;  // KS > 1
+  const float* att;   // KS == 1
+  const float* w;
+  const float* bias;
+  const float* res;
+  const float* g;
+  const float* beta;
+  float* out;
+  int H, D, P, KS, ld;
+  float eps;
+};
+bool attn_out_ln_supported(int H, int D, int KS);
+void launch_attn_out_ln(const AttnOutArgs& a, int B, hipStream_t s);
 
 // Op-level attention on head-interleaved [T][C] q/k/v (head h in columns
 // [h*D, (h+1)*D)); used [2T-1][D] (relative table, m = s - t + T - 1) or null.

@@ -93,7 +93,65 @@ struct Synth : SessionBase {
   float* dec_har = nullptr;  // the harmonic source of the current call (side stream)
   std::vector<float*> dec_noise;
 
+  // ---- deferred calls (rvc_synth_submit / _collect / _abort) ----
+  // Each outstanding call owns a pinned host staging buffer and an event
+  // recorded after its waveform's device-to-host copy; the calls share the
+  // workspace, which the one engine stream keeps in order.
+  struct Pending {
+    long long id = 0;  // 0: free
+    float* host = nullptr;
+    size_t cap = 0;    // floats
+    hipEvent_t done = nullptr;
+    long long n = 0;   // floats of this call's waveform
+  };
+  std::vector<Pending> pend;
+  long long next_ticket = 1;
+  static constexpr int kMaxPending = 8;
+  void pending_room() const {
+    int busy = 0;
+    for (const Pending& p : pend) busy += p.id != 0;
+    RVC_CHECK(busy < kMaxPending, "submit: too many outstanding calls (collect or abort some first)");
+  }
+  // reserve a free slot for a call whose work is already queued
+  Pending& pending_slot(long long n) {
+    Pending* slot = nullptr;
+    for (Pending& p : pend)
+      if (p.id == 0) {
+        slot = &p;
+        break;
+      }
+    if (!slot) {
+      RVC_CHECK((int)pend.size() < kMaxPending, "submit: too many outstanding calls (collect or abort some first)");
+      pend.emplace_back();
+      slot = &pend.back();
+      RVC_HIP(hipEventCreateWithFlags(&slot->done, hipEventDisableTiming));
+    }
+    if (slot->cap < (size_t)n) {
+      if (slot->host) RVC_HIP(hipHostFree(slot->host));
+      slot->host = nullptr;
+      slot->cap = 0;
+      RVC_HIP(hipHostMalloc((void**)&slot->host, sizeof(float) * std::max<long long>(n, 1), hipHostMallocDefault));
+      slot->cap = (size_t)n;
+    }
+    slot->id = next_ticket++;
+    slot->n = n;
+    return *slot;
+  }
+  Pending& pending_find(long long id) {
+    for (Pending& p : pend)
+      if (id > 0 && p.id == id) return p;
+    RVC_CHECK(false, "collect: unknown or already collected ticket");
+    return pend.front();  // not reached
+  }
+
   ~Synth() override {
+    for (Pending& p : pend) {
+      if (p.done) {
+        (void)hipEventSynchronize(p.done);
+        (void)hipEventDestroy(p.done);
+      }
+      if (p.host) (void)hipHostFree(p.host);
+    }
     if (side) (void)hipStreamSynchronize(side);
     if (forked) (void)hipEventDestroy(forked);
     if (joined) (void)hipEventDestroy(joined);
@@ -396,6 +454,24 @@ struct Synth : SessionBase {
         [&] { launch_gather_rows_i64(sid, emb_g, g, B, n_spk, gin, errw, eng->stream); });
   }
 
+  // Whether enc_p runs the fused five-launch layers: fp32, at least one
+  // layer, H within the staged-LayerNorm 1x1 kernel and the fused attention
+  // output kernel, P within the whole-reduction kernels' column limit.
+  bool fused_layers(int P) const {
+    return precision == 0 && n_layers > 0 && H <= 256 && H % 8 == 0 && P <= 8192 &&
+           attn_out_ln_supported(heads, kc, relpos_attention_splits(heads, kc, P, kWindow, true));
+  }
+  // a 1x1 conv whose input is the un-normalised sum before layer L's second
+  // LayerNorm: normalise while staging, and store the normalised tensor
+  static void stage_ln(ConvLaunch& c, const EncL& L, float* out, long long HP, int P) {
+    c.ln_g = L.g2;
+    c.ln_b = L.b2;
+    c.ln_out = out;
+    c.ln_ob = HP;
+    c.ln_oc = P;
+    c.ln_eps = 1e-5f;
+  }
+
   // enc_p: embedding, the attention / FFN layers and proj, then
   // z_p = m + exp(logs) * nz * 0.66666 -> [B][H][P] (batch stride H*P).
   float* encode(const float* phone, const long long* pitch, const float* nz, int B, int P) {
@@ -417,6 +493,59 @@ struct Synth : SessionBase {
     float* f = buf("ffn", (size_t)B * F * P);
     const size_t apart_n = std::max<size_t>(1, relpos_attention_scratch_floats(B, heads, kc, P, kWindow, true));
     float* apart = buf("attn_part", apart_n);
+    if (fused_layers(P)) {
+      // Five launches per layer: q/k/v (with the previous layer's second
+      // LayerNorm applied while its input is staged; its C_out tile 0 also
+      // stores the normalised tensor, the layer's residual), the attention,
+      // merge + conv_o + residual + LayerNorm in one kernel, the two FFN
+      // convs (the second adds the residual and leaves its sum
+      // un-normalised for the next consumer).  proj applies the last
+      // LayerNorm the same way and stores enc_out.
+      float* x1 = buf("enc_x1", (size_t)B * HP);
+      const int KS = relpos_attention_splits(heads, kc, P, kWindow, true);
+      for (int i = 0; i < n_layers; ++i) {
+        const EncL& L = enc[i];
+        ConvLaunch cq = c1x1(i == 0 ? xin : o, HP, L.wqkv, L.bqkv, qkv, B, H, 3 * H, P);
+        if (i > 0) stage_ln(cq, enc[i - 1], xo, HP, P);
+        conv("enc.qkv", cq);
+        run("enc.attn", 4.0 * B * heads * (double)P * P * kc, 4.0 * B * 4 * HP, [&] {
+          const int ks = launch_relpos_attention_partials(qkv, L.ek, L.ev, att, apart, apart_n, B, heads, kc, P,
+                                                          kWindow, s);
+          RVC_CHECK(ks == KS, "encode: attention key split changed");
+        });
+        AttnOutArgs ao{};
+        ao.part = apart;
+        ao.att = att;
+        ao.w = L.wo;
+        ao.bias = L.bo;
+        ao.res = i == 0 ? xin : xo;
+        ao.g = L.g1;
+        ao.beta = L.b1;
+        ao.out = x1;
+        ao.H = heads;
+        ao.D = kc;
+        ao.P = P;
+        ao.KS = KS;
+        ao.ld = packed_ld(H);
+        ao.eps = 1e-5f;
+        const double in_bytes = KS > 1 ? 4.0 * B * heads * KS * (kc + 2.0) * P : 4.0 * B * HP;
+        run("enc.o", 2.0 * B * H * (double)H * P, in_bytes + 4.0 * (3.0 * B * HP + (double)H * H),
+            [&] { launch_attn_out_ln(ao, B, s); });
+        ConvLaunch c1 = cargs_same(x1, HP, P, L.w1, L.bf1, f, (long long)F * P, P, B, H, F, P, 3, 1, 1);
+        c1.out_act = ACT_RELU;
+        conv("enc.ffn", c1);
+        ConvLaunch c2 = cargs_same(f, (long long)F * P, P, L.w2, L.bf2, o, HP, P, B, F, H, P, 3, 1, 1);
+        c2.g[0].res = x1; c2.rb = HP; c2.rc = P;
+        conv("enc.ffn", c2);
+      }
+      float* st = buf("stats", (size_t)B * 2 * HP);
+      ConvLaunch cp = c1x1(o, HP, proj_w, proj_b, st, B, H, 2 * H, P);
+      stage_ln(cp, enc[n_layers - 1], xo, HP, P);
+      conv("enc.proj", cp);
+      float* zp = buf("z_p", (size_t)B * HP);
+      run("enc.glue", 3.0 * B * HP, 16.0 * B * HP, [&] { launch_zp(st, nz, zp, B, H, P, 0.66666f, s); });
+      return zp;
+    }
     const float* x = xin;
     for (int i = 0; i < n_layers; ++i) {
       const EncL& L = enc[i];
@@ -772,7 +901,11 @@ struct Synth : SessionBase {
     p.in_act = ACT_LEAKY; p.in_slope = 0.01f;
     p.out_act = ACT_TANH;
     p.combine = COMB_STORE; p.div = 1.f; p.B = B;
-    run("dec.post", 2.0 * B * c_in * 7.0 * L, 4.0 * B * ((double)c_in * L + L), [&] { launch_conv1d_direct(p, s); });
+    // bytes: every input channel of each input read once (the three ResBlock
+    // outputs when the average is folded in), the wave written once
+    const double n_in = fold_avg ? 3.0 : 1.0;
+    run("dec.post", 2.0 * B * c_in * 7.0 * L, 4.0 * B * (n_in * c_in * L + L) + 4.0 * 7.0 * c_in,
+        [&] { launch_conv1d_direct(p, s); });
   }
 
   void check_ready() const { RVC_CHECK(ready, "synth session not finalized"); }
@@ -889,6 +1022,77 @@ int32_t rvc_synth_infer_dev(int64_t sh, int64_t phone, int64_t pitch, int64_t ns
     e.sync();
     s.collect_timing();
     s.check_ids();
+  });
+}
+
+namespace {
+void check_ids_host(const Synth& s, const int64_t* pitch, const int64_t* sid, long long B, long long P);
+}  // namespace
+
+int64_t rvc_synth_submit(int64_t sh, const float* phone, int64_t phone_buf, const int64_t* pitch,
+                         const float* nsff0, const int64_t* sid, const float* nz, const float* ns, int64_t B,
+                         int64_t P) {
+  int64_t ticket = -1;
+  const int32_t rc = sguard(sh, [&](Synth& s) {
+    s.check_ready();
+    s.check_BP(B, P);
+    RVC_CHECK((phone != nullptr) != (phone_buf != 0), "submit: pass exactly one of phone and phone_buf");
+    RVC_CHECK(pitch && nsff0 && sid && nz && ns, "submit: null pointer");
+    check_ids_host(s, pitch, sid, B, P);
+    hipStream_t st = s.eng->stream;
+    const long long N = P * s.upp;
+    const float* d_ph = nullptr;
+    if (phone_buf != 0) {
+      d_ph = s.eng->fptr(phone_buf, B * P * s.phone_dim, "submit phone_buf");
+    } else {
+      float* d = s.buf("in_phone", (size_t)(B * P * s.phone_dim));
+      RVC_HIP(hipMemcpyAsync(d, phone, sizeof(float) * B * P * s.phone_dim, hipMemcpyHostToDevice, st));
+      d_ph = d;
+    }
+    float* d_pitch = s.buf("in_pitch", (size_t)(B * P * 2));
+    float* d_f0 = s.buf("in_f0", (size_t)(B * P));
+    float* d_sid = s.buf("in_sid", (size_t)(B * 2));
+    float* d_nz = s.buf("in_nz", (size_t)(B * s.H * P));
+    float* d_ns = s.buf("in_ns", (size_t)(B * N));
+    float* d_w = s.buf("out_wave", (size_t)(B * N));
+    s.pending_room();
+    RVC_HIP(hipMemcpyAsync(d_pitch, pitch, 8 * B * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_sid, sid, 8 * B, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
+    RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
+    float* g = s.buf("g", (size_t)B * s.gin);
+    s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
+    s.decode_prep(g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P);
+    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g);
+    s.decode_main(z, (long long)s.H * P, (int)B, (int)P, d_w);
+    s.close_span();
+    Synth::Pending& slot = s.pending_slot(B * N);
+    RVC_HIP(hipMemcpyAsync(slot.host, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
+    RVC_HIP(hipEventRecord(slot.done, st));
+    ticket = slot.id;
+  });
+  return rc == 0 ? ticket : -1;
+}
+
+int32_t rvc_synth_collect(int64_t sh, int64_t ticket, float* wave) {
+  return sguard(sh, [&](Synth& s) {
+    RVC_CHECK(wave != nullptr, "collect: null pointer");
+    Synth::Pending& p = s.pending_find(ticket);
+    const hipError_t e = hipEventSynchronize(p.done);
+    const long long n = p.n;
+    if (e == hipSuccess) std::memcpy(wave, p.host, sizeof(float) * n);
+    p.id = 0;  // the slot is free again, whatever the outcome
+    RVC_HIP(e);
+  });
+}
+
+int32_t rvc_synth_abort(int64_t sh, int64_t ticket) {
+  return sguard(sh, [&](Synth& s) {
+    Synth::Pending& p = s.pending_find(ticket);
+    const hipError_t e = hipEventSynchronize(p.done);
+    p.id = 0;
+    RVC_HIP(e);
   });
 }
 

@@ -111,6 +111,9 @@ SYMBOLS = {
     "rvc_synth_set_weight": (I32, [I64, CHARP, F32P, I64P, I32]),
     "rvc_synth_finalize": (I32, [I64, I64, I64P, I64P, I32]),
     "rvc_synth_infer": (I32, [I64, F32P, I64P, F32P, I64P, F32P, F32P, I64, I64, F32P]),
+    "rvc_synth_submit": (I64, [I64, F32P, I64, I64P, F32P, I64P, F32P, F32P, I64, I64]),
+    "rvc_synth_collect": (I32, [I64, I64, F32P]),
+    "rvc_synth_abort": (I32, [I64, I64]),
     "rvc_synth_infer_dev": (I32, [I64] * 10),
     "rvc_synth_decode": (I32, [I64, F32P, F32P, F32P, F32P, I64, I64, F32P]),
     "rvc_synth_decode_dev": (I32, [I64] * 8),

@@ -29,7 +29,7 @@ from . import _hip
 from .config import VitsConfig
 from .hip_ops import HipContext, get_context
 
-__all__ = ["HipSynthesizer"]
+__all__ = ["HipSynthesizer", "HipDeferred"]
 
 _F32P = ctypes.POINTER(ctypes.c_float)
 _I64P = ctypes.POINTER(ctypes.c_int64)
@@ -71,6 +71,54 @@ class HipGenerator:
         """Chunks of any lengths, one speaker g (``:1847-1878``); each result
         equals ``forward`` of that chunk bit for bit."""
         return self._s.decode_chunks(z_list, g, f0_list, ns_list, off_list)
+
+
+class HipDeferred:
+    """The holder ``infer(..., _defer=True)`` returns (the reference's
+    ``_DecCollector``, ``runtime/models/vits.py:1314-1360``): the synthesis
+    is queued on the GPU; ``collect()`` waits for it and returns the waveform,
+    ``abort()`` waits and drops it.  Either ends the holder; a second call
+    raises ``RuntimeError``.  A holder dropped without either is aborted.
+    It keeps the resident phone buffer alive until the call is ended."""
+
+    __slots__ = ("_s", "_ticket", "_shape", "_keep", "_done")
+
+    def __init__(self, synth, ticket, shape, keep):
+        self._s = synth
+        self._ticket = ticket
+        self._shape = shape
+        self._keep = keep
+        self._done = False
+
+    def collect(self):
+        if self._done:
+            raise RuntimeError("HipDeferred: already collected or aborted")
+        self._done = True
+        wave = np.empty(self._shape, dtype=np.float32)
+        try:
+            _hip._check(self._s._lib.rvc_synth_collect(self._s.handle, self._ticket, wave.ctypes.data_as(_F32P)),
+                        "rvc_synth_collect")
+        finally:
+            self._keep = None
+        return wave
+
+    def abort(self):
+        if self._done:
+            return
+        self._done = True
+        try:
+            self._s._lib.rvc_synth_abort(self._s.handle, self._ticket)
+        finally:
+            self._keep = None
+
+    def __del__(self):
+        try:
+            import sys
+
+            if not sys.is_finalizing() and not self._done and self._s.handle:
+                self.abort()
+        except Exception:  # noqa: BLE001
+            pass
 
 
 class HipSynthesizer:
@@ -138,31 +186,59 @@ class HipSynthesizer:
         ns = rng.standard_normal((1, P * self.cfg.upp, 1)).astype(np.float32)
         return nz, ns
 
-    def infer(self, phone, pitch, nsff0, sid, seed=None, skip_head=None, return_length=None):
+    def infer(self, phone, pitch, nsff0, sid, seed=None, skip_head=None, return_length=None, phone_gpu=None,
+              _defer: bool = False):
         """``SynthesizerTrn.infer`` (``:2352-2402``): full synthesis, or with
         ``skip_head`` / ``return_length`` the waveform of frames
-        [skip_head, skip_head + return_length) from the partial path."""
+        [skip_head, skip_head + return_length) from the partial path.
+        ``phone_gpu`` / ``_defer`` as in ``infer_controlled``; the partial
+        path ignores ``_defer`` and returns the waveform, as the reference's
+        does."""
         P = np.asarray(phone).shape[1]
         nz, ns = self.make_noise(P, seed)
         if skip_head is None or return_length is None:
-            return self.infer_controlled(phone, pitch, nsff0, sid, nz, ns)
+            return self.infer_controlled(phone, pitch, nsff0, sid, nz, ns, phone_gpu=phone_gpu, _defer=_defer)
         head, length = self._check_part(P, skip_head, return_length)
         p = self._partial_prep(phone, pitch, nsff0, sid, nz, ns, head, length)
         o = self.dec.forward(p["z_seg"], p["nsff0_seg"], p["g"], p["ns_seg"], seg_offsets=p["off"])
         return o[:, :, p["s0"]:p["s0"] + p["n_out"]]
 
-    def infer_controlled(self, phone, pitch, nsff0, sid, nz, ns):
+    def infer_controlled(self, phone, pitch, nsff0, sid, nz, ns, phone_gpu=None, _defer: bool = False):
         """phone [B,P,D], pitch int [B,P], nsff0 [B,P], sid int [1] or [B],
-        nz [B,hidden,P], ns [B,P*upp(,1)] -> wave [B,1,P*upp]."""
+        nz [B,hidden,P], ns [B,P*upp(,1)] -> wave [B,1,P*upp].
+
+        ``phone_gpu``: a resident ``hip_ops.PersistentBuffer`` of this
+        session's context holding ``phone`` ([1,P,D] or [P,D] floats); the
+        encoder reads it instead of uploading ``phone`` (the reference's
+        ``phone_gpu``, ``runtime/models/vits.py:2352-2402``).  A freed
+        buffer, one of another context or one too small is ignored and
+        ``phone`` is uploaded.  ``_defer=True`` queues the synthesis and
+        returns a holder whose ``collect()`` waits and returns the waveform
+        (``abort()`` drops it), so the host can prepare the next chunk while
+        the GPU runs this one (``:2551-2595``, ``runtime/pipeline.py:
+        1010-1080``); up to 8 calls may be outstanding."""
         phone, pitch, nsff0, sid, nz = self._enc_inputs(phone, pitch, nsff0, sid, nz)
         B, P, _ = phone.shape
         ns = _f32(ns).reshape(B, P * self.cfg.upp)
-        wave = np.empty((B, 1, P * self.cfg.upp), dtype=np.float32)
-        _hip._check(self._lib.rvc_synth_infer(
-            self.handle, phone.ctypes.data_as(_F32P), pitch.ctypes.data_as(_I64P), nsff0.ctypes.data_as(_F32P),
-            sid.ctypes.data_as(_I64P), nz.ctypes.data_as(_F32P), ns.ctypes.data_as(_F32P), B, P,
-            wave.ctypes.data_as(_F32P)), "rvc_synth_infer")
-        return wave
+        buf = 0
+        if phone_gpu is not None and getattr(phone_gpu, "valid", False) and getattr(phone_gpu, "_ctx", None) is \
+                self.ctx and int(getattr(phone_gpu, "nbytes", 0)) >= phone.nbytes:
+            buf = int(phone_gpu.id)
+        if not _defer and not buf:
+            wave = np.empty((B, 1, P * self.cfg.upp), dtype=np.float32)
+            _hip._check(self._lib.rvc_synth_infer(
+                self.handle, phone.ctypes.data_as(_F32P), pitch.ctypes.data_as(_I64P),
+                nsff0.ctypes.data_as(_F32P), sid.ctypes.data_as(_I64P), nz.ctypes.data_as(_F32P),
+                ns.ctypes.data_as(_F32P), B, P, wave.ctypes.data_as(_F32P)), "rvc_synth_infer")
+            return wave
+        ticket = int(self._lib.rvc_synth_submit(
+            self.handle, None if buf else phone.ctypes.data_as(_F32P), buf, pitch.ctypes.data_as(_I64P),
+            nsff0.ctypes.data_as(_F32P), sid.ctypes.data_as(_I64P), nz.ctypes.data_as(_F32P),
+            ns.ctypes.data_as(_F32P), B, P))
+        if ticket < 0:
+            raise RuntimeError(f"rvc_synth_submit failed: {_hip.last_error()}")
+        holder = HipDeferred(self, ticket, (B, 1, P * self.cfg.upp), phone_gpu if buf else None)
+        return holder if _defer else holder.collect()
 
     def _enc_inputs(self, phone, pitch, nsff0, sid, nz):
         phone = _f32(phone)
