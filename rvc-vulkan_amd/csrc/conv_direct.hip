@@ -140,10 +140,11 @@ __global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
 // Requirements (checked by the launcher): L % 4 == 0 and 16-byte aligned
 // rows, so each aligned float4 lies wholly inside [0, L) or wholly outside,
 // and outside ones read 0 through the buffer range.
-constexpr int kPostTile = 1024, kPostCh = 4, kPostW = kPostTile + 8;
-template <int K>
-__global__ __launch_bounds__(256) void conv_post_kernel(DirectConvArgs a) {
-  __shared__ float4 win[2][kPostCh][kPostW / 4];
+constexpr int kPostCh = 4;
+template <int K, int NT, int CH>
+__global__ __launch_bounds__(NT) void conv_post_kernel(DirectConvArgs a) {
+  constexpr int kPostTile = 4 * NT, kPostW = kPostTile + 8;
+  __shared__ float4 win[2][CH][kPostW / 4];
   const int tid = threadIdx.x;
   const int b = blockIdx.y;
   const int t0 = blockIdx.x * kPostTile;
@@ -152,18 +153,18 @@ __global__ __launch_bounds__(256) void conv_post_kernel(DirectConvArgs a) {
   const __amdgpu_buffer_rsrc_t r0 = uniform_rsrc(a.x + (long long)b * a.xb, range);
   const __amdgpu_buffer_rsrc_t r1 = uniform_rsrc(nin == 3 ? a.x2 + (long long)b * a.xb : a.x, range);
   const __amdgpu_buffer_rsrc_t r2 = uniform_rsrc(nin == 3 ? a.x3 + (long long)b * a.xb : a.x, range);
-  // window float4 f covers samples t0 - 4 + 4f .. + 3: f = tid, and f = 256 + tid for tid < 2
+  // window float4 f covers samples t0 - 4 + 4f .. + 3: f = tid, and f = NT + tid for tid < 2
   auto foff = [&](int f, int c) -> unsigned {
     const int t = t0 - 4 + 4 * f;
     return (t >= 0 && t < a.L_in) ? 4u * (unsigned)(c * (int)a.xc + t) : kBufOut;
   };
   const bool halo = tid < 2;
-  float4 v[3][kPostCh], h[3][kPostCh];
+  float4 v[3][CH], h[3][CH];
   auto load = [&](int c0) {
 #pragma unroll
-    for (int r = 0; r < kPostCh; ++r) {
+    for (int r = 0; r < CH; ++r) {
       const unsigned o = foff(tid, c0 + r);
-      const unsigned oh = halo ? foff(256 + tid, c0 + r) : kBufOut;
+      const unsigned oh = halo ? foff(NT + tid, c0 + r) : kBufOut;
       v[0][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r0, o, 0, 0));
       if (halo) h[0][r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r0, oh, 0, 0));
       if (nin == 3) {
@@ -189,24 +190,24 @@ __global__ __launch_bounds__(256) void conv_post_kernel(DirectConvArgs a) {
   };
   constexpr int c_off = 4 - (K - 1) / 2;  // window column of output 4t's first tap, minus 4t
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const int ng = a.C_in / kPostCh;
+  const int ng = a.C_in / CH;
   load(0);
   for (int g = 0; g < ng; ++g) {
     const int buf = g & 1;
 #pragma unroll
-    for (int r = 0; r < kPostCh; ++r) {
+    for (int r = 0; r < CH; ++r) {
       win[buf][r][tid] = prep(v[0][r], v[1][r], v[2][r]);
-      if (halo) win[buf][r][256 + tid] = prep(h[0][r], h[1][r], h[2][r]);
+      if (halo) win[buf][r][NT + tid] = prep(h[0][r], h[1][r], h[2][r]);
     }
     __syncthreads();
-    if (g + 1 < ng) load((g + 1) * kPostCh);
+    if (g + 1 < ng) load((g + 1) * CH);
 #pragma unroll
-    for (int r = 0; r < kPostCh; ++r) {
+    for (int r = 0; r < CH; ++r) {
       const float* wl = reinterpret_cast<const float*>(&win[buf][r][0]) + 4 * tid + c_off;
       float x[K + 3];
 #pragma unroll
       for (int i = 0; i < K + 3; ++i) x[i] = wl[i];
-      const float* wr = a.w + (long long)(g * kPostCh + r) * K;
+      const float* wr = a.w + (long long)(g * CH + r) * K;
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const float wv = wr[k];
@@ -409,12 +410,13 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
     dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);
     hipLaunchKernelGGL(conv1d_direct_kernel<8>, grid, dim3(256), 0, s, a);
   } else if (conv_post_ok(a)) {
-    dim3 grid((a.n_out + kPostTile - 1) / kPostTile, a.B);
+    constexpr int NT = 256, CH = kPostCh;
+    dim3 grid((a.n_out + 4 * NT - 1) / (4 * NT), a.B);
     switch (a.K) {
-      case 3: hipLaunchKernelGGL(conv_post_kernel<3>, grid, dim3(256), 0, s, a); break;
-      case 5: hipLaunchKernelGGL(conv_post_kernel<5>, grid, dim3(256), 0, s, a); break;
-      case 7: hipLaunchKernelGGL(conv_post_kernel<7>, grid, dim3(256), 0, s, a); break;
-      default: hipLaunchKernelGGL(conv_post_kernel<9>, grid, dim3(256), 0, s, a); break;
+      case 3: hipLaunchKernelGGL((conv_post_kernel<3, NT, CH>), grid, dim3(NT), 0, s, a); break;
+      case 5: hipLaunchKernelGGL((conv_post_kernel<5, NT, CH>), grid, dim3(NT), 0, s, a); break;
+      case 7: hipLaunchKernelGGL((conv_post_kernel<7, NT, CH>), grid, dim3(NT), 0, s, a); break;
+      default: hipLaunchKernelGGL((conv_post_kernel<9, NT, CH>), grid, dim3(NT), 0, s, a); break;
     }
   } else if (a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax) {
     dim3 grid((a.n_out + kRowOut - 1) / kRowOut, a.C_out, a.B);

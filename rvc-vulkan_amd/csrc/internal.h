@@ -284,8 +284,12 @@ struct ConvTOsLaunch {
   const float* noise;                           // [B][C_out][L_out] (strides ob, oc) or null
   const float* har; long long harb; long long N;  // harmonic source [B][N]
   const float* nw; const float* nb; int kn, ns, np;  // noise conv [C_out][kn], [C_out]
+  // bf16 operands (w16 set): weights [K][C_out][w16_ld] in bf16, the input
+  // rounded to bf16 after the leaky ReLU, fp32 accumulate; w / w_ld unused
+  const uint16_t* w16; int w16_ld;
 };
-// (K, S) shapes the kernel is instantiated for: (16, 10), (20, 10), (24, 12), (4, 2)
+// (K, S) shapes the kernel is instantiated for: (16, 10), (20, 10), (24, 12), (4, 2);
+// the bf16 form needs C_in % 32 == 0 as well
 bool convt_os_supported(int K, int S);
 // false when no instantiation fits (C_out / C_in multiples)
 bool launch_convt_os(const ConvTOsLaunch& a, hipStream_t s);

@@ -77,6 +77,9 @@ struct Synth : SessionBase {
     // fp32 output-stationary ConvTranspose (convt_os_supported shapes): all
     // taps packed [K][C_in][packed_ld(C)]; null when the polyphase grids run
     float* up_all = nullptr;
+    // bf16 output-stationary ConvTranspose (precision >= 1): all taps packed
+    // [K][C_out][bf16_ld(C_in)] in bf16; null when the polyphase grids run
+    uint16_t* up_all16 = nullptr;
     bool noise_fused = false;  // the stage's noise conv is computed by that kernel
   };
   std::vector<StageW> stages;
@@ -388,7 +391,7 @@ struct Synth : SessionBase {
               ph[((size_t)jp * c_in + ci) * ld + co] = wt[((size_t)ci * c + co) * K + k];
         }
         S.phases.push_back(upload(ph));
-        if (b16) {
+        if (b16 && !(convt_os_supported(K, st) && c_in % 32 == 0 && c % 32 == 0)) {
           const int ld16 = bf16_ld(c_in);
           std::vector<uint16_t> p16((size_t)J * c * ld16, 0);
           for (int jp = 0; jp < J; ++jp) {
@@ -413,6 +416,16 @@ struct Synth : SessionBase {
           for (int ci = 0; ci < c_in; ++ci)
             for (int co = 0; co < c; ++co) all[((size_t)k * c_in + ci) * ld + co] = wt[((size_t)ci * c + co) * K + k];
         S.up_all = upload(all);
+        S.noise_fused = kn <= kNoiseTapsMax;
+      }
+      if (b16 && convt_os_supported(K, st) && c_in % 32 == 0 && c % 32 == 0) {
+        const int ld16 = bf16_ld(c_in);
+        std::vector<uint16_t> all16((size_t)K * c * ld16, 0);  // [k][co][ci] = bf16(wt[ci][co][k])
+        for (int k = 0; k < K; ++k)
+          for (int co = 0; co < c; ++co)
+            for (int ci = 0; ci < c_in; ++ci)
+              all16[((size_t)k * c + co) * ld16 + ci] = f32_to_bf16(wt[((size_t)ci * c + co) * K + k]);
+        S.up_all16 = upload16(all16);
         S.noise_fused = kn <= kNoiseTapsMax;
       }
       S.nw = upload_key(nc + ".weight");
@@ -800,12 +813,14 @@ struct Synth : SessionBase {
         std::vector<const float*> ph(stages[i].phases.begin(), stages[i].phases.end());
         std::snprintf(tg, sizeof tg, "dec.ups.s%d", i);
         const StageW& SW = stages[i];
-        if (SW.up_all) {
+        if (SW.up_all || SW.up_all16) {
           // one output-stationary launch: ConvTranspose + bias + the noise
-          // term (computed from har, or read from the side stream's buffer)
+          // term (computed from har, or read from the side stream's buffer),
+          // on fp32 or (precision >= 1) bf16 operands
           ConvTOsLaunch o{};
           o.x = cur; o.xb = (long long)c_in * L; o.L_in = L;
           o.w = SW.up_all; o.w_ld = packed_ld(C); o.bias = SW.up_b;
+          o.w16 = SW.up_all16; o.w16_ld = bf16_ld(c_in);
           o.out = X; o.ob = CL; o.oc = Lo; o.L_out = Lo;
           o.B = B; o.C_in = c_in; o.C_out = C; o.K = K; o.S = st; o.pad = pad;
           o.M = (Lo + pad + st - 1) / st;

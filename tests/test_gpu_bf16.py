@@ -10,8 +10,9 @@ really happened.
 
 Synthesis level (the tolerance config 5 states): waveform
 SNR = 10 log10(sum ref^2 / sum (y - ref)^2) >= 40 dB against the fp32 numpy
-oracle at 1 s, and against the fp32 HIP path at config 5's full size
-(4 independent seeds x 10 s, batch 4).  Mode 2 (ResBlocks also bf16) is
+oracle at 1 s and at config 5's full size (4 independent seeds x 10 s,
+batch 4), and against the fp32 HIP path at full size.  The bf16
+upsamplers are also checked stage by stage against an exact emulation.  Mode 2 (ResBlocks also bf16) is
 reported separately; its SNR is recorded, with a loose floor."""
 
 from __future__ import annotations
@@ -142,6 +143,72 @@ def test_config5_1s_snr_vs_oracle():
     for b, i in enumerate(ins):
         want = ref.infer_controlled(i["phone"], i["pitch"], i["nsff0"], i["sid"], i["nz"], i["ns"])
         assert snr_db(y[b:b + 1], want) >= 40.0
+
+
+def test_bf16_upsamplers_match_exact_emulation():
+    """Mode 1's upsamplers run the output-stationary ConvTranspose on bf16
+    operands, the noise conv fused in fp32.  Stage by stage, from the GPU's
+    own stage input: leaky ReLU, operands rounded to bf16, the transposed
+    convolution summed in float64, + bias + the fp32 noise conv, then the fp32
+    ResBlocks; the GPU's stage output must match at rel L2 2e-5 (fp32
+    summation order only) and differ from the unrounded fp32 result by
+    bf16-sized amounts."""
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=4)
+    s = _synth(w, geom, 1)
+    s.set_debug(True)
+    P = 40
+    inp = syn.make_synth_inputs(geom, P, seed=77)
+    s.infer_controlled(inp["phone"], inp["pitch"], inp["nsff0"], inp["sid"], inp["nz"], inp["ns"])
+    ref = V.Synthesizer(w, sr=geom.sr)
+    cfg = ref.cfg
+    U = w["dec.conv_pre.weight"].shape[0]
+    har = s.read("har", (1, P * geom.upp))[:, None, :]
+    L = P
+    for i in range(cfg.n_ups):
+        C = U >> (i + 1)
+        xh = s.read(f"dec_stage{i - 1}" if i > 0 else "dec_pre", (1, U >> i, L))
+        y = nn.leaky_relu(xh, 0.1)
+        up = f"dec.ups.{i}"
+        wt = V.deweight_norm(w[up + ".weight_v"], w[up + ".weight_g"])
+        st, K = cfg.upsample_rates[i], cfg.upsample_kernels[i]
+        pad = (K - st) // 2
+        noise = nn.conv1d(har, w[f"dec.noise_convs.{i}.weight"], w[f"dec.noise_convs.{i}.bias"],
+                          stride=cfg.noise_strides[i], padding=cfg.noise_strides[i] // 2)
+        emu = nn.conv_transpose1d(bf16_round(y).astype(np.float64), bf16_round(wt).astype(np.float64), None,
+                                  stride=st, padding=pad) + w[up + ".bias"].astype(np.float64)[None, :, None]
+        full = nn.conv_transpose1d(y, wt, w[up + ".bias"], stride=st, padding=pad)
+        outs = []
+        for yy in (emu.astype(np.float32) + noise, full + noise):
+            xs = None
+            for j, k in enumerate((3, 7, 11)):
+                o = V.resblock1(w, f"dec.resblocks.{3 * i + j}", k, yy)
+                xs = o if xs is None else xs + o
+            outs.append(xs / 3)
+        L *= st
+        got = s.read(f"dec_stage{i}", (1, C, L))
+        assert rel_l2(got, outs[0]) < 2e-5, f"stage {i}"
+        assert rel_l2(got, outs[1]) > 1e-4, f"stage {i}: no bf16 rounding visible"
+
+
+def test_config5_full_size_vs_oracle():
+    """BASELINE config 5 as stated: 4 independent seeds x 10 s as one batch of
+    4, upsamplers and enc_p matmuls on bf16, each wave against the fp32 numpy
+    oracle (taps formulation) at SNR >= 40 dB; the per-seed margin is
+    printed."""
+    geom = syn.GEOM_40K
+    w = syn.make_weights(geom, seed=0)
+    ins, cat = _stack_inputs(geom, 1000, (31, 32, 33, 34))
+    y = _synth(w, geom, 1).infer_controlled(cat["phone"], cat["pitch"], cat["nsff0"], cat["sid"], cat["nz"],
+                                           cat["ns"])
+    ref = V.Synthesizer(w, sr=geom.sr)
+    snrs = []
+    with nn.conv_formulation("taps"):
+        for b, i in enumerate(ins):
+            want = ref.infer_controlled(i["phone"], i["pitch"], i["nsff0"], i["sid"], i["nz"], i["ns"])
+            snrs.append(snr_db(y[b:b + 1], want))
+    print("config 5 SNR vs oracle per seed: " + ", ".join(f"{v:.2f} dB (margin {v - 40.0:+.2f})" for v in snrs))
+    assert min(snrs) >= 40.0
 
 
 def test_config5_full_size_snr():
