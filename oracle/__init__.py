@@ -40,4 +40,25 @@ than itself; the tests named here live under ``tests/``):
   ``GeneratorNSF.forward`` and ``Synthesizer.infer_controlled``: golden
   vectors produced by the reference's own numpy code at reduced and full
   width (``tests/golden/*.npz``; test_oracle_golden.py).
+* ``Synthesizer.make_noise`` (nz drawn before ns from one
+  ``RandomState(seed)``, ``RVC_FIXED_SEED``), ``infer(seed)``,
+  ``phase_offsets``, ``sine_gen(seg_offsets)``, the partial ``prep_dec``
+  (flow from ``max(head - 40, 0)``, decoder segment +- 16 frames),
+  ``decode_batch(preps)`` over unequal chunks and
+  ``infer(skip_head, return_length)``: the reference's own outputs for each
+  (``tests/golden/make_golden_partial.py``; test_oracle_partial.py).
+  ``phase_offsets`` is also compared bit for bit with the GPU's blocked scan
+  at 16 383 - 70 001 frames (test_gpu_partial.py).
+* the ``conv_formulation("taps")`` form of ``nn_ref.conv1d`` /
+  ``conv_transpose1d`` (contiguous per-tap GEMMs, used by the full-size
+  parity tests for speed): agrees with the default einsum form (the
+  reference's sliding window with zero-stuffed dilation) and with the
+  float64 loops on every decoder, flow and encoder op shape
+  (test_oracle_ops.py).
+* ``pipeline_ref`` (``vc_prepare``, ``search_l2``, ``change_rms``,
+  interpolation, protect, int16) and ``rmvpe_ref`` (log-mel, U-Net,
+  BiGRU, decode): the reference's own outputs written by
+  ``tests/golden/make_golden_pipeline.py`` / ``make_golden_rmvpe.py``, plus
+  torch routines and float64 loops where those leave a case open
+  (test_oracle_pipeline.py, test_oracle_rmvpe.py).
 """

@@ -26,6 +26,7 @@
 // MFMA with fp32 accumulate; 2 = mode 1 plus the
 // decoder ResBlock convs on bf16.  Everything else stays fp32.
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <cstring>
 
@@ -487,7 +488,11 @@ struct Synth : SessionBase {
 
   // enc_p: embedding, the attention / FFN layers and proj, then
   // z_p = m + exp(logs) * nz * 0.66666 -> [B][H][P] (batch stride H*P).
-  float* encode(const float* phone, const long long* pitch, const float* nz, int B, int P) {
+  // before_zp (optional) runs on the host once every enc_p kernel but z_p is
+  // queued: the host-input path uploads nz (and the decoder's f0 / noise)
+  // there, so those copies overlap the encoder on the GPU.
+  float* encode(const float* phone, const long long* pitch, const float* nz, int B, int P,
+                const std::function<void()>& before_zp = {}) {
     hipStream_t s = eng->stream;
     const long long HP = (long long)H * P;
     float* phT = buf("phT", (size_t)B * phone_dim * P);
@@ -556,7 +561,8 @@ struct Synth : SessionBase {
       stage_ln(cp, enc[n_layers - 1], xo, HP, P);
       conv("enc.proj", cp);
       float* zp = buf("z_p", (size_t)B * HP);
-      run("enc.glue", 3.0 * B * HP, 16.0 * B * HP, [&] { launch_zp(st, nz, zp, B, H, P, 0.66666f, s); });
+      if (before_zp) before_zp();
+    run("enc.glue", 3.0 * B * HP, 16.0 * B * HP, [&] { launch_zp(st, nz, zp, B, H, P, 0.66666f, s); });
       return zp;
     }
     const float* x = xin;
@@ -581,6 +587,7 @@ struct Synth : SessionBase {
     float* st = buf("stats", (size_t)B * 2 * HP);
     conv("enc.proj", with16(c1x1(x, HP, proj_w, proj_b, st, B, H, 2 * H, P), proj16));
     float* zp = buf("z_p", (size_t)B * HP);
+    if (before_zp) before_zp();
     run("enc.glue", 3.0 * B * HP, 16.0 * B * HP, [&] { launch_zp(st, nz, zp, B, H, P, 0.66666f, s); });
     return zp;
   }
@@ -688,8 +695,9 @@ struct Synth : SessionBase {
   }
 
   // enc_p + flow over all P frames (infer_controlled's z)
-  const float* enc_flow(const float* phone, const long long* pitch, const float* nz, int B, int P, const float* g) {
-    return flow(encode(phone, pitch, nz, B, P), B, P, g);
+  const float* enc_flow(const float* phone, const long long* pitch, const float* nz, int B, int P, const float* g,
+                        const std::function<void()>& before_zp = {}) {
+    return flow(encode(phone, pitch, nz, B, P, before_zp), B, P, g);
   }
 
   // enc_p over all P frames, then the flow over frames [flow_head, P) only:
@@ -1071,15 +1079,17 @@ int64_t rvc_synth_submit(int64_t sh, const float* phone, int64_t phone_buf, cons
     float* d_ns = s.buf("in_ns", (size_t)(B * N));
     float* d_w = s.buf("out_wave", (size_t)(B * N));
     s.pending_room();
+    // as in rvc_synth_infer: nz, f0 and the NSF noise upload behind the encoder
     RVC_HIP(hipMemcpyAsync(d_pitch, pitch, 8 * B * P, hipMemcpyHostToDevice, st));
-    RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_sid, sid, 8 * B, hipMemcpyHostToDevice, st));
-    RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
-    RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
     float* g = s.buf("g", (size_t)B * s.gin);
     s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
-    s.decode_prep(g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P);
-    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g);
+    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g, [&] {
+      RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
+      RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+      RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
+      s.decode_prep(g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P);
+    });
     s.decode_main(z, (long long)s.H * P, (int)B, (int)P, d_w);
     s.close_span();
     Synth::Pending& slot = s.pending_slot(B * N);
@@ -1135,16 +1145,21 @@ int32_t rvc_synth_infer(int64_t sh, const float* phone, const int64_t* pitch, co
     float* d_nz = s.buf("in_nz", (size_t)(B * s.H * P));
     float* d_ns = s.buf("in_ns", (size_t)(B * N));
     float* d_w = s.buf("out_wave", (size_t)(B * N));
+    // The encoder needs only phone, pitch and sid: they go first, the
+    // encoder is queued, and the host then uploads nz, f0 and the NSF noise
+    // while the GPU runs it (pageable copies return once staged, in stream
+    // order before z_p and the decoder's source that read them).
     RVC_HIP(hipMemcpyAsync(d_ph, phone, sizeof(float) * B * P * s.phone_dim, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_pitch, pitch, 8 * B * P, hipMemcpyHostToDevice, st));
-    RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
     RVC_HIP(hipMemcpyAsync(d_sid, sid, 8 * B, hipMemcpyHostToDevice, st));
-    RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
-    RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
     float* g = s.buf("g", (size_t)B * s.gin);
     s.speaker(reinterpret_cast<const long long*>(d_sid), (int)B, g);
-    s.decode_prep(g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P);
-    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g);
+    const float* z = s.enc_flow(d_ph, reinterpret_cast<const long long*>(d_pitch), d_nz, (int)B, (int)P, g, [&] {
+      RVC_HIP(hipMemcpyAsync(d_nz, nz, sizeof(float) * B * s.H * P, hipMemcpyHostToDevice, st));
+      RVC_HIP(hipMemcpyAsync(d_f0, nsff0, sizeof(float) * B * P, hipMemcpyHostToDevice, st));
+      RVC_HIP(hipMemcpyAsync(d_ns, ns, sizeof(float) * B * N, hipMemcpyHostToDevice, st));
+      s.decode_prep(g, s.gin, d_f0, d_ns, nullptr, (int)B, (int)P);
+    });
     s.decode_main(z, (long long)s.H * P, (int)B, (int)P, d_w);
     s.close_span();
     RVC_HIP(hipMemcpyAsync(wave, d_w, sizeof(float) * B * N, hipMemcpyDeviceToHost, st));
