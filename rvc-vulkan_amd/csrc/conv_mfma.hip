@@ -580,7 +580,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     const float* ws = xs + (DIRECT ? XREG : BKT * XW);
     const float* wbase = ws + half * BM + wm * WM + l32;
     const float* xbase = xs + half * XW + wn * WN + l32;
-    float av[2][TM], bv[2][TN];
+    float av[4][TM], bv[4][TN];
     auto lda = [&](int k, int q, int p) {
       const float* w_ = wbase + (k * BKT + 2 * q) * BM;
       const float* x_ = xbase + 2 * q * XW + k * dil;
@@ -589,15 +589,23 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
 #pragma unroll
       for (int n = 0; n < TN; ++n) bv[p][n] = x_[n * 32];
     };
+    // LDS operands run PD MFMA steps ahead of their use (three for the 32-row
+    // tiles of stages 0 and 3, two for the 64-row tiles of stages 1-2, each
+    // measured best for its tile), in a ring of four slots: with BK / 2 = 4
+    // steps per tap the slot of step q is q itself, a compile-time index
+    static_assert(BK / 2 == 4, "four steps per tap: the ring slot of a step is its q");
+    constexpr int PD = BM == 32 ? 3 : 2;
     lda(0, 0, 0);
+    lda(0, 1, 1);
+    if (PD == 3) lda(0, 2, 2);
     for (int k = 0; k < K; ++k) {
 #pragma unroll
       for (int q = 0; q < BK / 2; ++q) {
-        const int p = q & 1;
-        if (q + 1 < BK / 2)
-          lda(k, q + 1, p ^ 1);
+        const int p = q;
+        if (q + PD < BK / 2)
+          lda(k, q + PD, q + PD);
         else
-          lda(k + 1 < K ? k + 1 : k, 0, p ^ 1);
+          lda(k + 1 < K ? k + 1 : k, q + PD - BK / 2, (q + PD) & 3);
 #pragma unroll
         for (int m = 0; m < TM; ++m)
 #pragma unroll
