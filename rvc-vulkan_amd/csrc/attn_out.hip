@@ -202,8 +202,7 @@ void launch_rt(const AttnOutArgs& a, dim3 grid, hipStream_t s) {
 
 bool attn_out_ln_supported(int H, int D, int KS) {
   const int C = H * D;
-  return (C == 64 || C == 96 || C == 128 || C == 192 || C == 256) && KS >= 1 && KS <= kMaxKS &&
-         H * BN <= 4 * C;
+  return H >= 1 && D >= 1 && (C == 64 || C == 96 || C == 128 || C == 192 || C == 256) && KS >= 1 && KS <= kMaxKS;
 }
 
 void launch_attn_out_ln(const AttnOutArgs& a, int B, hipStream_t s) {

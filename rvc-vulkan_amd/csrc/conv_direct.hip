@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void conv1d_rows_kernel(DirectConvArgs a) {
         float v = 0.f;
         if (t >= 0 && t < a.L_in) {
           v = xb[ro + t];
-          if (xb2) v = ((v + xb2[ro + t]) + xb3[ro + t]) / 3.0f;  // the decoder's ((o1 + o2) + o3) / 3
+          if (xb2) v = div3_rn((v + xb2[ro + t]) + xb3[ro + t]);  // the decoder's ((o1 + o2) + o3) / 3
           v = act_in(v, a.in_act, a.in_slope);
         }
         rows[r][c] = v;
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(NT) void conv_post_kernel(DirectConvArgs a) {
     if (nin == 3) {
       const float f[4] = {y.x, y.y, y.z, y.w}, g[4] = {z.x, z.y, z.z, z.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) e[i] = ((e[i] + f[i]) + g[i]) / 3.0f;  // the decoder's ((o1 + o2) + o3) / 3
+      for (int i = 0; i < 4; ++i) e[i] = div3_rn((e[i] + f[i]) + g[i]);  // the decoder's ((o1 + o2) + o3) / 3
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) e[i] = act_in(e[i], a.in_act, a.in_slope);

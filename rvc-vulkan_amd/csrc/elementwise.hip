@@ -64,7 +64,7 @@ __global__ void bias_add_kernel(float* o, const float* a, const float* bias, lon
   GRID_STRIDE(i, n) o[i] = a[i] + bias[i % cols];
 }
 __global__ void avg3_kernel(float* o, const float* a, const float* b, const float* c, long long n) {
-  GRID_STRIDE(i, n) o[i] = ((a[i] + b[i]) + c[i]) / 3.0f;
+  GRID_STRIDE(i, n) o[i] = div3_rn((a[i] + b[i]) + c[i]);
 }
 
 // ids are validated by the host; the clamp only keeps a bad device-resident

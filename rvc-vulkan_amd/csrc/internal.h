@@ -69,6 +69,20 @@ __device__ __forceinline__ void buffer_load_lds_b128(__amdgpu_buffer_rsrc_t r, f
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
 }
 
+// x / 3 rounded to nearest (the decoder's ResBlock average) in five VALU
+// operations instead of the full division sequence: q0 = RN(x * r) with
+// r = RN(1/3), the remainder x - 3 q0 by one fused multiply-add, and
+// q = RN(q0 + remainder * r).  q is bit-identical to the IEEE quotient for
+// every finite non-zero float (all 2^32 bit patterns checked on the host);
+// zeros and infinities, where the remainder is 0 or NaN, take q0, which is
+// then the exact quotient with its sign.
+__device__ __forceinline__ float div3_rn(float x) {
+  constexpr float r = 0x1.555556p-2f;
+  const float q0 = __fmul_rn(x, r);
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, 3.0f, x), r, q0);
+  return (q0 == 0.f || __builtin_isinf(q0)) ? q0 : q;
+}
+
 // logistic function in the two-branch form of runtime/nn.py:520-523
 __device__ inline float sigmoid_as(float x) {
   if (x >= 0.f) return 1.0f / (1.0f + expf(-x));
