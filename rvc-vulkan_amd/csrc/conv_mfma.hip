@@ -760,9 +760,64 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
 // channels cb + r, rows [16, 32) channels H + cb + r - 16, and
 // out[c] = tanh(v_c + g_c) * sigmoid(v_{H+c} + g_{H+c}) for the 16 channels
 // (v including the bias), g per batch item.
+// Mean and 1 / den of a LayerNorm over C channels for column i0 + tid % BN,
+// from the float64 (sum, sum of squares) of ntile 32-row tiles, double2
+// [B][ntile][L] (ConvLaunch::stat_out).  NP = NT / BN threads per column:
+// thread (p, col) adds tiles p, p + NP, ... with all its loads in flight,
+// then one thread adds the NP partials in p order -- a fixed grouping, so
+// the result depends on the statistics only.  mean = S / C, var = (Q - S *
+// mean) / C, den = sqrt(var + eps) (the LayerNorm kernels' formulas with the
+// two passes folded into the sums).  scratch: NT double2 + 2 BN floats of
+// LDS; two barriers, every thread of the workgroup calls it.  Columns past L
+// get 0, 0.
+template <int NT, int BN>
+__device__ __forceinline__ void ln_column_stats(const double* stat, int ntile, int C, int L, float eps, int b, int i0,
+                                                float* scratch, float& mu, float& rd) {
+  constexpr int NP = NT / BN;
+  constexpr int kMaxPer = 4;  // tiles per thread: ntile <= NP * kMaxPer (checked by the launcher)
+  const int tid = threadIdx.x;
+  const int col = tid % BN, p = tid / BN;
+  const int i = i0 + col;
+  const bool icol = i < L;
+  double2* part = reinterpret_cast<double2*>(scratch);
+  float* out = reinterpret_cast<float*>(part + NT);
+  const double2* st = reinterpret_cast<const double2*>(stat) + (long long)b * ntile * L + i;
+  double2 v[kMaxPer];
+#pragma unroll
+  for (int u = 0; u < kMaxPer; ++u) {
+    const int t = p + NP * u;
+    v[u] = icol && t < ntile ? st[(long long)t * L] : make_double2(0.0, 0.0);
+  }
+  double S = 0.0, Q = 0.0;
+#pragma unroll
+  for (int u = 0; u < kMaxPer; ++u) {
+    S += v[u].x;
+    Q += v[u].y;
+  }
+  part[tid] = make_double2(S, Q);
+  __syncthreads();
+  if (tid < BN) {
+    S = 0.0;
+    Q = 0.0;
+    for (int q = 0; q < NP; ++q) {
+      const double2 w = part[q * BN + tid];
+      S += w.x;
+      Q += w.y;
+    }
+    const double md = S / C;
+    out[tid] = (float)md;
+    out[BN + tid] = 1.0f / sqrtf((float)(fmax(Q - S * md, 0.0) / C) + eps);
+  }
+  __syncthreads();
+  mu = icol ? out[col] : 0.f;
+  rd = icol ? out[BN + col] : 0.f;
+  __syncthreads();  // the scratch is free again
+}
+
 template <int BN, int NW = 4>
 __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const ConvGroup& G, int b, int i0, int co0,
-                                                    bool gate, const floatx16 (&acc)[BN / 32], float* red) {
+                                                    bool gate, const floatx16 (&acc)[BN / 32], float* red, float rs_mu,
+                                                    float rs_rd) {
   constexpr int TN = BN / 32;
   constexpr int RS = 64 * NW / BN;
   constexpr int KO = 32 * BN / (64 * NW);
@@ -839,6 +894,17 @@ __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const C
     const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(rb, 4u * (unsigned)((a.C_out - 1) * (int)a.rc + G.n_out));
 #pragma unroll
     for (int k = 0; k < KO; ++k) rv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ro[k], 0, 0));
+    if (a.res_stat) {
+      // the residual's LayerNorm (column statistics from the kernel start)
+      const __amdgpu_buffer_rsrc_t gs = uniform_rsrc(a.res_g, 4u * (unsigned)a.C_out);
+      const __amdgpu_buffer_rsrc_t bs = uniform_rsrc(a.res_b, 4u * (unsigned)a.C_out);
+#pragma unroll
+      for (int k = 0; k < KO; ++k) {
+        const float g = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(gs, bo[k], 0, 0));
+        const float be = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(bs, bo[k], 0, 0));
+        rv[k] = (rv[k] - rs_mu) * rs_rd * g + be;
+      }
+    }
   }
   if (G.combine != COMB_STORE) {
 #pragma unroll
@@ -859,6 +925,25 @@ __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const C
       t = ov[k] - t;
     }
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, t), ors, oo[k], 0, 0);
+    v[k] = t;
+  }
+  if (a.stat_out) {
+    // the next LayerNorm's column statistics of this tile: the 32 stored
+    // values of each column through LDS, added in row order by one thread
+    __syncthreads();  // every thread has read its partial tiles
+#pragma unroll
+    for (int k = 0; k < KO; ++k) red[(tid / BN + k * RS) * BN + col] = v[k];
+    __syncthreads();
+    if (tid < BN && icol) {
+      double sm = 0.0, sq = 0.0;
+#pragma unroll 8
+      for (int r = 0; r < 32; ++r) {
+        const double x = red[r * BN + tid];
+        sm += x;
+        sq += x * x;
+      }
+      reinterpret_cast<double2*>(a.stat_out)[((long long)b * gridDim.y + blockIdx.y) * G.n_out + i] = make_double2(sm, sq);
+    }
   }
 }
 
@@ -1044,7 +1129,7 @@ __global__ __launch_bounds__(256) void conv1x1_small_kernel(ConvLaunch a) {
     for (int n = 0; n < TN; ++n)
       acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, xl[2 * st * BN + n * 32], acc[n], 0, 0, 0);
   }
-  small_conv_epilogue<BN>(a, G, b, i0, co0, false, acc, smem);
+  small_conv_epilogue<BN>(a, G, b, i0, co0, false, acc, smem, 0.f, 0.f);
 }
 
 // K-tap convs (K = 3, 5 or 7, dilation 1, stride 1), C_in % CHK == 0: the
@@ -1129,14 +1214,33 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
   const float* wl = ws + (wave * Q + half) * 32 + l32;
   const float* xl = xs + (wave * Q + half) * XW + l32;
   load(0);
+  // LayerNorms from the producers' column statistics (1x1 launches only;
+  // a thread stages and finishes one column, tid % BN): of the input while
+  // it is staged (no affine: the caller folds gamma / beta into the weights
+  // and bias), and of the residual in the epilogue.  xs is free until the
+  // first chunk is staged and holds the statistics' scratch.
+  constexpr bool kLn = K == 1;
+  static_assert(!kLn || (NT % BN == 0 && XE * NT >= 4 * NT + 2 * BN), "a thread stages one column; scratch room");
+  const bool ln = kLn && a.ln_stat != nullptr;
+  float ln_mu = 0.f, ln_rd = 0.f, rs_mu = 0.f, rs_rd = 0.f;
+  if constexpr (kLn) {
+    if (ln) ln_column_stats<NT, BN>(a.ln_stat, a.ln_ntile, C_in, a.L_in, a.ln_eps, b, i0, xs, ln_mu, ln_rd);
+    if (a.res_stat)
+      ln_column_stats<NT, BN>(a.res_stat, a.C_out / 32, a.C_out, G.n_out, a.ln_eps, b, i0, xs, rs_mu, rs_rd);
+  }
   for (int c = 0; c < n_ch; ++c) {
 #pragma unroll
     for (int j = 0; j < WF4; ++j) reinterpret_cast<float4*>(ws)[j * NT + tid] = wv[j];
+    if (ln) {
 #pragma unroll
-    for (int j = 0; j < XE; ++j) {
-      float u = xv[j];
-      if (leaky) u = u >= 0.f ? u : u * a.in_slope;
-      xs[j * NT + tid] = u;
+      for (int j = 0; j < XE; ++j) xs[j * NT + tid] = (xv[j] - ln_mu) * ln_rd;
+    } else {
+#pragma unroll
+      for (int j = 0; j < XE; ++j) {
+        float u = xv[j];
+        if (leaky) u = u >= 0.f ? u : u * a.in_slope;
+        xs[j * NT + tid] = u;
+      }
     }
     __syncthreads();
     if (c + 1 < n_ch) load(c + 1);
@@ -1156,7 +1260,7 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
     }
     if (c + 1 < n_ch) __syncthreads();  // the next chunk's stores overwrite this one
   }
-  small_conv_epilogue<BN, NW>(a, G, b, i0, co0, gate, acc, smem);
+  small_conv_epilogue<BN, NW>(a, G, b, i0, co0, gate, acc, smem, rs_mu, rs_rd);
 }
 
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
@@ -1436,8 +1540,10 @@ void launch_small_conv_cfg(const ConvLaunch& a, dim3 grid, hipStream_t s) {
   constexpr int XE = (CHK * (BN + K - 1) + NT - 1) / NT;
   constexpr size_t lds_stage = sizeof(float) * ((size_t)K * CHK * 32 + (size_t)XE * NT);
   constexpr size_t lds_red = sizeof(float) * NW * (BN / 32) * 16 * 64;  // the epilogue's partial tiles
+  static_assert((lds_stage > lds_red ? lds_stage : lds_red) <= 160 * 1024, "staging LDS above the CU's 160 KiB");
+  RVC_CHECK((!a.ln_stat || a.ln_ntile <= 4 * (NT / BN)) && (!a.res_stat || a.C_out / 32 <= 4 * (NT / BN)),
+            "conv_small: too many statistics tiles for a staged LayerNorm");
   constexpr size_t lds = lds_stage > lds_red ? lds_stage : lds_red;
-  static_assert(lds <= 160 * 1024, "staging LDS above the CU's 160 KiB");
   // the gate epilogue pairs tile rows k and k + KO / 2 of one thread
   RVC_CHECK(a.post != POST_WN_GATE || 32 * BN / (64 * NW) >= 2,
             "conv_small: the WaveNet gate needs at least two tile rows per thread");
@@ -1610,6 +1716,11 @@ bool conv1d_mfma_supported(int K, int dil) {
   return K >= 0 && K <= kConvTapsMax && dil >= 1 && (K > 0 ? (K - 1) * dil : 0) <= kConvHaloMax;
 }
 
+bool conv1d_mfma_chunked_1x1(const ConvLaunch& a) {
+  return a.n_groups == 1 && a.g[0].K == 1 && (a.g[0].in_step <= 1) && a.post == POST_NONE && !small_gemm_ok(a) &&
+         small_conv_ok(a);
+}
+
 void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   RVC_CHECK(a.n_groups >= 1 && a.n_groups <= kMaxConvGroups, "conv1d_mfma: bad group count");
   RVC_CHECK(a.C_in >= 1 && a.C_out >= 1 && a.B >= 1 && a.w_ld >= a.C_out && a.w_ld % 4 == 0,
@@ -1625,8 +1736,19 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
     RVC_CHECK((reinterpret_cast<uintptr_t>(a.g[g].w) & 15) == 0, "conv1d_mfma: weights must be 16-byte aligned");
   }
   if (max_n_out(a) == 0) return;
-  RVC_CHECK(!a.ln_g || (step == 1 && small_gemm_ok(a)),
-            "conv1d_mfma: a staged LayerNorm needs the whole-reduction 1x1 kernel (C_in <= 256, <= 8192 columns)");
+  if (a.ln_stat) {
+    RVC_CHECK(conv1d_mfma_chunked_1x1(a) && a.in_act == ACT_NONE && a.ln_ntile >= 1 && a.ln_ntile * 32 == a.C_in,
+              "conv1d_mfma: a LayerNorm from producer statistics needs the chunked 1x1 kernel (one group, no input "
+              "activation, C_in / 32 statistics tiles)");
+  } else {
+    RVC_CHECK(!a.ln_g || (step == 1 && small_gemm_ok(a)),
+              "conv1d_mfma: a staged LayerNorm needs the whole-reduction 1x1 kernel (C_in <= 256, <= 8192 columns)");
+  }
+  RVC_CHECK(!a.stat_out || (step == 1 && a.n_groups == 1 && a.C_out % 32 == 0 && a.post == POST_NONE &&
+                            (small_gemm_ok(a) || small_conv_ok(a))),
+            "conv1d_mfma: column statistics need a small-conv kernel (one group, C_out % 32 == 0)");
+  RVC_CHECK(!a.res_stat || (conv1d_mfma_chunked_1x1(a) && a.C_out % 32 == 0 && a.g[0].res && a.res_g && a.res_b),
+            "conv1d_mfma: a residual LayerNorm needs the chunked 1x1 kernel, a residual, gamma and beta");
   if (step == 1 && small_gemm_ok(a) && launch_small_gemm(a, s)) return;
   if (step == 1 && small_conv_ok(a) && launch_small_conv(a, s)) return;
   for (int g = 0; g < a.n_groups; ++g)

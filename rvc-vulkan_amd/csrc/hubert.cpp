@@ -41,6 +41,10 @@ struct Hubert : SessionBase {
   float *pos_b = nullptr, *enc_ln_g = nullptr, *enc_ln_b = nullptr;
   struct Layer {
     float *wqkv, *bqkv, *wo, *bo, *ln1_g, *ln1_b, *wi, *bi, *wf, *bf, *ln2_g, *ln2_b;
+    // the LayerNorm in front folded in, W diag(g) and b + W beta: the FFN
+    // input GEMM with LN1, the q/k/v GEMM with the previous layer's LN2
+    // (null for layer 0, whose input the encoder's LayerNorm launch forms)
+    float *wi_ln, *bi_ln, *wqkv_ln, *bqkv_ln;
   };
   std::vector<Layer> layers;
   float *final_w = nullptr, *final_b = nullptr;
@@ -51,6 +55,25 @@ struct Hubert : SessionBase {
     const HostT& t = W(key + ".weight");
     check_shape(key + ".weight", t.shape, {O, I});
     return upload(pack(t.data, O, I, 1));
+  }
+
+  // A linear layer [O][I] (+ bias [O]) behind a LayerNorm with affine g, beta
+  // over its I inputs, folded: W'[o][i] = W[o][i] * g[i] (float32 product),
+  // b'[o] = b[o] + sum_i W[o][i] * beta[i] (float64 sum, rounded once).
+  // Uploads the packed W' and returns b' uploaded through *bias.
+  float* upload_folded(const std::vector<float>& w, const std::vector<float>& b, const std::vector<float>& g,
+                       const std::vector<float>& beta, long long O, long long I, float** bias) {
+    std::vector<float> wf(w.size()), bf(O);
+    for (long long o = 0; o < O; ++o) {
+      double acc = 0.0;
+      for (long long i = 0; i < I; ++i) {
+        wf[o * I + i] = w[o * I + i] * g[i];
+        acc += (double)w[o * I + i] * beta[i];
+      }
+      bf[o] = (float)((double)b[o] + acc);
+    }
+    *bias = upload(bf);
+    return upload(pack(wf, O, I, 1));
   }
 
   void finalize() {
@@ -158,12 +181,19 @@ struct Hubert : SessionBase {
       }
       L.wqkv = upload(pack(qkv, 3 * H, H, 1));
       L.bqkv = upload(bqkv);
+      if (i > 0) {
+        const std::string q = "encoder.layers." + std::to_string(i - 1) + ".final_layer_norm.";
+        L.wqkv_ln = upload_folded(qkv, bqkv, W(q + "weight").data, W(q + "bias").data, 3 * H, H, &L.bqkv_ln);
+      }
       L.wo = upload_linear(p + "attention.out_proj", H, H);
       L.bo = upload_vec(p + "attention.out_proj.bias", H);
       L.ln1_g = upload_vec(p + "layer_norm.weight", H);
       L.ln1_b = upload_vec(p + "layer_norm.bias", H);
       L.wi = upload_linear(p + "feed_forward.intermediate_dense", F, H);
       L.bi = upload_vec(p + "feed_forward.intermediate_dense.bias", F);
+      L.wi_ln = upload_folded(W(p + "feed_forward.intermediate_dense.weight").data,
+                              W(p + "feed_forward.intermediate_dense.bias").data, W(p + "layer_norm.weight").data,
+                              W(p + "layer_norm.bias").data, F, H, &L.bi_ln);
       L.wf = upload_linear(p + "feed_forward.output_dense", H, F);
       L.bf = upload_vec(p + "feed_forward.output_dense.bias", H);
       L.ln2_g = upload_vec(p + "final_layer_norm.weight", H);
@@ -276,29 +306,88 @@ struct Hubert : SessionBase {
     float* xb_ = buf("xb", (size_t)B * HL);
     const size_t part_n = std::max<size_t>(1, relpos_attention_scratch_floats(B, kHeads, D, (int)L, 0, false));
     float* part = buf("attn_part", part_n);
-    const float* cur = x0;
     const int nl = version == 1 ? 9 : n_layers;
+    // Post-LN layers: x1 = LN1(x + o-proj(attn)), x' = LN2(x1 + FFN(x1)).
+    // When the four 1x1 GEMMs of a layer run on the chunked small-conv
+    // kernel (L up to about 950 frames), neither LayerNorm is a launch of its
+    // own and no normalised tensor is stored: the o-projection and the FFN
+    // output GEMM also write the column statistics of their 32-row tiles
+    // (st1, st2), the FFN input / next q/k/v GEMM normalise their input while
+    // staging it, and the GEMM that adds the normalised tensor as its
+    // residual normalises the raw one in its epilogue.  Only the last
+    // layer's LN2 is a LayerNorm launch.  Longer inputs (split-K GEMMs) keep
+    // the LayerNorm launches.
+    const int nt = H / 32;
+    double* st1 = reinterpret_cast<double*>(buf("ln_stat1", (size_t)4 * B * nt * L));
+    double* st2 = reinterpret_cast<double*>(buf("ln_stat2", (size_t)4 * B * nt * L));
+    float* t2 = buf("t2", (size_t)B * HL);
+    bool fold = H % 32 == 0;
+    {
+      const ConvLaunch probe[4] = {c1x1(x0, HL, layers[0].wqkv, layers[0].bqkv, qkv, B, H, 3 * H, (int)L),
+                                   c1x1(att, HL, layers[0].wo, layers[0].bo, t1, B, H, H, (int)L),
+                                   c1x1(t1, HL, layers[0].wi, layers[0].bi, ff, B, H, F, (int)L),
+                                   c1x1(ff, (long long)F * L, layers[0].wf, layers[0].bf, t2, B, F, H, (int)L)};
+      for (const ConvLaunch& p : probe) fold = fold && conv1d_mfma_chunked_1x1(p);
+    }
+    auto ln_in = [&](ConvLaunch& c, const double* st) {  // the affine is in the folded weights
+      c.ln_stat = st;
+      c.ln_ntile = nt;
+      c.ln_eps = 1e-5f;
+    };
+    auto ln_res = [&](ConvLaunch& c, const double* st, const float* g, const float* bt) {
+      c.res_stat = st;
+      c.res_g = g;
+      c.res_b = bt;
+      c.ln_eps = 1e-5f;
+    };
+    const float* cur = x0;       // the layer input, normalised
+    const float* raw = nullptr;  // fold: the previous layer's FFN sum before its LN2 (statistics in st2)
     for (int i = 0; i < nl; ++i) {
       const Layer& Ly = layers[i];
+      const Layer* Lp = i > 0 ? &layers[i - 1] : nullptr;
       float* xo = (i & 1) ? xb_ : xa;
-      conv("hub.qkv", c1x1(cur, HL, Ly.wqkv, Ly.bqkv, qkv, B, H, 3 * H, (int)L));
+      ConvLaunch cq = raw ? c1x1(raw, HL, Ly.wqkv_ln, Ly.bqkv_ln, qkv, B, H, 3 * H, (int)L)
+                          : c1x1(cur, HL, Ly.wqkv, Ly.bqkv, qkv, B, H, 3 * H, (int)L);
+      if (raw) ln_in(cq, st2);
+      conv("hub.qkv", cq);
       run("hub.attn", 4.0 * B * kHeads * (double)L * L * D, 4.0 * B * 4.0 * HL,
           [&] { launch_relpos_attention(qkv, nullptr, nullptr, att, part, part_n, B, kHeads, D, (int)L, 0, s); });
       ConvLaunch co = c1x1(att, HL, Ly.wo, Ly.bo, t1, B, H, H, (int)L);
-      co.g[0].res = cur; co.rb = HL; co.rc = L;
+      co.g[0].res = raw ? raw : cur; co.rb = HL; co.rc = L;
+      if (raw) ln_res(co, st2, Lp->ln2_g, Lp->ln2_b);
+      if (fold) co.stat_out = st1;
       conv("hub.o", co);
-      run("hub.ln", 8.0 * B * HL, 8.0 * B * HL,
-          [&] { launch_layernorm_cols(t1, Ly.ln1_g, Ly.ln1_b, x1, B, H, (int)L, 1e-5f, s); });
-      ConvLaunch fi = c1x1(x1, HL, Ly.wi, Ly.bi, ff, B, H, F, (int)L);
+      ConvLaunch fi{};
+      if (fold) {
+        fi = c1x1(t1, HL, Ly.wi_ln, Ly.bi_ln, ff, B, H, F, (int)L);
+        ln_in(fi, st1);
+      } else {
+        run("hub.ln", 8.0 * B * HL, 8.0 * B * HL,
+            [&] { launch_layernorm_cols(t1, Ly.ln1_g, Ly.ln1_b, x1, B, H, (int)L, 1e-5f, s); });
+        fi = c1x1(x1, HL, Ly.wi, Ly.bi, ff, B, H, F, (int)L);
+      }
       fi.out_act = ACT_GELU;
       conv("hub.ffn", fi);
-      ConvLaunch fo = c1x1(ff, (long long)F * L, Ly.wf, Ly.bf, t1, B, F, H, (int)L);
-      fo.g[0].res = x1; fo.rb = HL; fo.rc = L;
+      float* sum = fold ? t2 : t1;
+      ConvLaunch fo = c1x1(ff, (long long)F * L, Ly.wf, Ly.bf, sum, B, F, H, (int)L);
+      fo.g[0].res = fold ? t1 : x1; fo.rb = HL; fo.rc = L;
+      if (fold) ln_res(fo, st1, Ly.ln1_g, Ly.ln1_b);
+      const bool next_folds = fold && i + 1 < nl;
+      if (next_folds) fo.stat_out = st2;
       conv("hub.ffn", fo);
-      run("hub.ln", 8.0 * B * HL, 8.0 * B * HL,
-          [&] { launch_layernorm_cols(t1, Ly.ln2_g, Ly.ln2_b, xo, B, H, (int)L, 1e-5f, s); });
-      if (keep && i == 0) launch_copy(buf("layer1", (size_t)B * HL), xo, (long long)B * HL, s);
-      cur = xo;
+      if (next_folds) {
+        raw = t2;
+        // debug: the layer's output, normalised by a LayerNorm launch (the
+        // pipeline itself never stores it)
+        if (keep && i == 0)
+          launch_layernorm_cols(t2, Ly.ln2_g, Ly.ln2_b, buf("layer1", (size_t)B * HL), B, H, (int)L, 1e-5f, s);
+      } else {
+        run("hub.ln", 8.0 * B * HL, 8.0 * B * HL,
+            [&] { launch_layernorm_cols(sum, Ly.ln2_g, Ly.ln2_b, xo, B, H, (int)L, 1e-5f, s); });
+        cur = xo;
+        raw = nullptr;
+        if (keep && i == 0) launch_copy(buf("layer1", (size_t)B * HL), xo, (long long)B * HL, s);
+      }
     }
     const int od = out_dim(version);
     const float* res = cur;

@@ -184,12 +184,37 @@ struct ConvLaunch {
   float* ln_out;
   long long ln_ob, ln_oc;
   float ln_eps;
+  // The same LayerNorm in the chunked small-conv kernel (1x1, single group),
+  // whose chunks cannot hold a whole column: the statistics come from the
+  // kernel that produced the input.  stat_out (producer, single group,
+  // C_out % 32 == 0): per batch item, 32-row C_out tile and output column,
+  // the float64 sum and sum of squares of the 32 values it stored, added in
+  // row order, as double2 [B][C_out / 32][n_out].  ln_stat (consumer): its
+  // input's statistics in that layout, ln_ntile = C_in / 32 tiles of L_in
+  // columns, added in tile order: mean = S / C_in, var = (Q - S * mean) /
+  // C_in, and x' = (x - mean) * (1 / sqrt(var + ln_eps)) while staging --
+  // without the affine, which the caller folds into the weights (W diag(g))
+  // and the bias (+ W b); ln_g / ln_b / ln_out unused.  res_stat: the
+  // residual is such a raw tensor too (C_out channels, C_out / 32 tiles,
+  // statistics over n_out columns), normalised with its affine res_g / res_b
+  // (and ln_eps) before it is added, so no kernel stores the normalised
+  // tensor.  The sums do not depend on the batch or the tile widths of any
+  // launch.
+  double* stat_out;
+  const double* ln_stat;
+  int ln_ntile;
+  const double* res_stat;
+  const float* res_g;
+  const float* res_b;
 };
 enum Post : int { POST_NONE = 0, POST_WN_GATE = 1, POST_WN_UPDATE = 2 };
 
 // MFMA implicit-GEMM conv1d (input stride 1 or 2, the same for every group
 // of a launch), K <= kConvTapsMax and (K-1)*dil <= kConvHaloMax.
 bool conv1d_mfma_supported(int K, int dil);
+// launch_conv1d_mfma would run `a` (stride 1) on the chunked small-conv
+// kernel as a 1x1 GEMM: the launches that can take ln_stat
+bool conv1d_mfma_chunked_1x1(const ConvLaunch& a);
 // Scratch floats a launch needs for split-K partial sums (0: no split).
 size_t conv1d_mfma_split_floats(const ConvLaunch& a);
 // Whether the launch, given post = POST_WN_GATE (post_H = C_out / 2), takes a

@@ -106,6 +106,19 @@ def test_long_input_feature_extractor_vs_oracle(sd, hub):
     assert rel_l2(feats, want) < TOL
 
 
+def test_long_input_layernorm_launches_vs_oracle(sd, hub):
+    """20 s of input (999 frames): the FFN input GEMM's tiles leave the
+    chunked small-conv kernel, so every LayerNorm runs as a launch of its own
+    instead of inside the neighbouring GEMMs (the path of shorter inputs,
+    which the tests above cover); the output against the oracle's."""
+    x = syn.make_hubert_input(320000, seed=10)
+    got = hub.encode(x, version=2)
+    want = H.HubertRef(sd).encode(x, version=2)
+    assert got.shape == want.shape == (1, 999, 768)
+    assert rel_l2(got, want) < TOL
+    assert np.abs(got - want).max() < 1e-3
+
+
 def test_full_size_batch_equals_per_chunk(hub):
     """Two 10 s chunks (499 frames: key-split attention) as a batch of 2
     equal the chunks encoded one by one, bit for bit."""
