@@ -475,6 +475,28 @@ struct AttnOutArgs {
 bool attn_out_ln_supported(int H, int D, int KS);
 void launch_attn_out_ln(const AttnOutArgs& a, int B, hipStream_t s);
 
+// The end of a reverse flow and the next flow's pre conv in one launch
+// (flow_tail.hip): skip' = skip + (W_rs acts + b_rs); x1 -= W_post skip' +
+// b_post; h = W_pre x1 + b_pre (skipped when w_pre is null).  acts, skip, h
+// [B][C][P] contiguous; x1 [HALF = C / 2][P] at batch stride xb; weights
+// packed [C_in][ld] (w[ci * ld + co]).
+struct FlowTailArgs {
+  const float* acts;
+  const float* skip;
+  const float* w_rs;
+  const float* b_rs;
+  const float* w_post;
+  const float* b_post;
+  float* x1;
+  long long xb;
+  const float* w_pre;
+  const float* b_pre;
+  float* h;
+  int P, ld_rs, ld_post, ld_pre;
+};
+bool flow_tail_supported(int C, int half);
+void launch_flow_tail(const FlowTailArgs& a, int C, int B, hipStream_t s);
+
 // Op-level attention on head-interleaved [T][C] q/k/v (head h in columns
 // [h*D, (h+1)*D)); used [2T-1][D] (relative table, m = s - t + T - 1) or null.
 //   scores [H][T][T] = q_h . (k_h + used[m])

@@ -616,13 +616,18 @@ struct Synth : SessionBase {
         [&] { RVC_HIP(hipMemcpyAsync(X, src, sizeof(float) * B * HP, hipMemcpyDeviceToDevice, s)); });
     run("flow.glue", 2.0 * B * gin * n_flows * GW, 4.0 * (B * gin + (double)(gin + 1 + B) * n_flows * GW),
         [&] { launch_gemv(flow_cond_w, flow_cond_b, g, gin, gv, n_flows * GW, B, (int)(n_flows * GW), gin, s); });
+    // Each flow's last res/skip conv, its post conv and the next flow's pre
+    // conv run as one launch (flow_tail.hip) where the channel count allows:
+    // the next flow's pre reads the half this flow updates.
+    const bool tail = flow_tail_supported(H, half) && 4.0 * H * P < 2147483648.0;
+    bool pre_done = false;
     for (int fi = n_flows - 1; fi >= 0; --fi) {
       const FlowL& L = flows[fi];
       const long long lo = 0, hi = (long long)half * P;  // channel offsets of X's halves
       const float* x0 = X + (L.rev ? hi : lo);
       float* x1 = X + (L.rev ? lo : hi);
       const float* gf = gv + (long long)fi * GW;
-      conv("flow.pre", c1x1(x0, HP, L.pre_w, L.pre_b, h, B, half, H, P));
+      if (!pre_done) conv("flow.pre", c1x1(x0, HP, L.pre_w, L.pre_b, h, B, half, H, P));
       for (int i = 0; i < kWnLayers; ++i) {
         // in-layer conv + gate: fused into the small-conv kernel's epilogue
         // or the split-K reduce when the conv takes one of those paths (it
@@ -644,6 +649,7 @@ struct Synth : SessionBase {
             launch_wn_gate(xi, 2 * HP, gf + (long long)i * 2 * H, n_flows * GW, acts, B, H, P, s);
           });
         }
+        if (tail && i + 1 == kWnLayers) break;  // the last res/skip conv runs in the flow tail
         // res/skip conv as one launch of two output groups over the same
         // input: rows [0, H) accumulate into h (h += rs[:H]), rows [H, 2H)
         // into skip (skip = rs[H:] on the first layer); the last layer has
@@ -669,6 +675,35 @@ struct Synth : SessionBase {
           cr.g[1].combine = i == 0 ? COMB_STORE : COMB_ADD;
         }
         conv("flow.rs", cr);
+      }
+      if (tail) {
+        constexpr int kl = kWnLayers - 1;
+        FlowTailArgs ta{};
+        ta.acts = acts;
+        ta.skip = skip;
+        ta.w_rs = L.rs_w[kl];
+        ta.b_rs = L.rs_b[kl];
+        ta.ld_rs = packed_ld(L.rs_out[kl]);
+        ta.w_post = L.post_w;
+        ta.b_post = L.post_b;
+        ta.ld_post = packed_ld(half);
+        ta.x1 = x1;
+        ta.xb = HP;
+        ta.P = P;
+        if (fi > 0) {
+          const FlowL& N = flows[fi - 1];
+          RVC_CHECK(N.rev != L.rev, "flow: the next flow must read the half this one updates");
+          ta.w_pre = N.pre_w;
+          ta.b_pre = N.pre_b;
+          ta.ld_pre = packed_ld(H);
+          ta.h = h;
+        }
+        const double nxt = fi > 0 ? (double)H * half : 0.0;
+        run("flow.tail", 2.0 * B * P * ((double)H * H + (double)half * H + nxt),
+            4.0 * ((double)B * P * (2.0 * H + 2.0 * half + (fi > 0 ? H : 0)) + (double)H * H + (double)half * H + nxt),
+            [&] { launch_flow_tail(ta, H, B, s); });
+        pre_done = fi > 0;
+        continue;
       }
       // x1 = x1 - (post(skip) + b), into X's other half (batch stride HP)
       ConvLaunch cp = c1x1(skip, HP, L.post_w, L.post_b, x1, B, H, half, P);
