@@ -52,14 +52,21 @@ __global__ __launch_bounds__(64 * RT) void attn_out_ln_kernel(AttnOutArgs a) {
   const int col = tid % BN;  // the column this thread merges, normalises and stores
   const bool cin = t0 + col < P;
 
-  // this wave's weights: A[row l16][k 4s + kq] = W[co0 + l16][4s + kq]
+  // this wave's weights: A[row l16][k 4s + kq] = W[co0 + l16][4s + kq], in
+  // lane order (pack_mfma_lanes): step group j is one float4 per lane, the
+  // wave's 64 of them contiguous
   const int co0 = wave * 16;
-  const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(a.w, 4u * (unsigned)(C * a.ld));
-  const unsigned wof = 4u * (unsigned)(kq * a.ld + co0 + l16);
+  const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(a.w, 4u * (unsigned)(C * C));
+  const unsigned wof = 16u * (unsigned)(wave * (C / 16) * 64 + lane);
   float wv[C / 4];
 #pragma unroll
-  for (int s = 0; s < C / 4; ++s)
-    wv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, wof, 16u * s * a.ld, 0));
+  for (int s = 0; s < C / 16; ++s) {
+    const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wrs, wof, 1024u * s, 0));
+    wv[4 * s] = v.x;
+    wv[4 * s + 1] = v.y;
+    wv[4 * s + 2] = v.z;
+    wv[4 * s + 3] = v.w;
+  }
   // epilogue operands: rows co0 + 4 kq + g, column t0 + l16
   const __amdgpu_buffer_rsrc_t rrs = uniform_rsrc(a.res + (long long)b * C * P, 4u * (unsigned)(C * P));
   float bias[4], rv[4];
@@ -209,7 +216,7 @@ void launch_attn_out_ln(const AttnOutArgs& a, int B, hipStream_t s) {
   const int C = a.H * a.D;
   RVC_CHECK(attn_out_ln_supported(a.H, a.D, a.KS), "attn_out_ln: unsupported channel count or key split");
   RVC_CHECK(a.KS == 1 ? a.att != nullptr : a.part != nullptr, "attn_out_ln: missing attention input");
-  RVC_CHECK(a.ld >= C && B >= 1 && a.P >= 1, "attn_out_ln: invalid shape");
+  RVC_CHECK(a.w && B >= 1 && a.P >= 1, "attn_out_ln: invalid shape");
   // 32-bit byte offsets: one batch item's partial slices and [C][P] tensors
   RVC_CHECK(4.0 * a.H * a.KS * (a.D + 2.0) * a.P < 2147483648.0 && 4.0 * C * a.P < 2147483648.0,
             "attn_out_ln: sequence too long for 32-bit offsets");

@@ -47,29 +47,25 @@ __global__ __launch_bounds__(64 * RT) void flow_tail_kernel(FlowTailArgs a) {
   const unsigned cp = 4u * (unsigned)P;  // bytes per channel row
 
   // ---- every global operand in flight at once ----
-  // weights: A[row l16][k 4s + kq] = W[4s + kq][co0 + l16] (packed [C_in][ld])
-  const __amdgpu_buffer_rsrc_t wr = uniform_rsrc(a.w_rs, 4u * (unsigned)(C * a.ld_rs));
-  const __amdgpu_buffer_rsrc_t wp = uniform_rsrc(a.w_post, 4u * (unsigned)(C * a.ld_post));
-  const __amdgpu_buffer_rsrc_t wq = uniform_rsrc(a.w_pre ? a.w_pre : a.w_post, 4u * (unsigned)(HALF * a.ld_pre));
+  // weights: A[row l16][k 4s + kq] = W[co0 + l16][4s + kq], in lane order
+  // (pack_mfma_lanes): step group j is one float4 per lane, the wave's 64 of
+  // them contiguous
   float wrv[C / 4], wpv[C / 4], wqv[HALF / 4];
-  {
-    const unsigned o = 4u * (unsigned)(kq * a.ld_rs + co0 + l16);
+  auto load_rows = [&](const float* w, int rows, int K, bool on, float* dst) {
+    const __amdgpu_buffer_rsrc_t rs = uniform_rsrc(w, 4u * (unsigned)(rows * K));
+    const unsigned o = on ? 16u * (unsigned)(wave * (K / 16) * 64 + lane) : kBufOut;
 #pragma unroll
-    for (int s = 0; s < C / 4; ++s)
-      wrv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, o, 16u * s * a.ld_rs, 0));
-  }
-  {
-    const unsigned o = wave < NPOST ? 4u * (unsigned)(kq * a.ld_post + co0 + l16) : kBufOut;
-#pragma unroll
-    for (int s = 0; s < C / 4; ++s)
-      wpv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wp, o, 16u * s * a.ld_post, 0));
-  }
-  {
-    const unsigned o = a.w_pre ? 4u * (unsigned)(kq * a.ld_pre + co0 + l16) : kBufOut;
-#pragma unroll
-    for (int s = 0; s < HALF / 4; ++s)
-      wqv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wq, o, 16u * s * a.ld_pre, 0));
-  }
+    for (int s = 0; s < K / 16; ++s) {
+      const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 1024u * s, 0));
+      dst[4 * s] = v.x;
+      dst[4 * s + 1] = v.y;
+      dst[4 * s + 2] = v.z;
+      dst[4 * s + 3] = v.w;
+    }
+  };
+  load_rows(a.w_rs, C, C, true, wrv);
+  load_rows(a.w_post, HALF, C, wave < NPOST, wpv);
+  load_rows(a.w_pre ? a.w_pre : a.w_post, C, HALF, a.w_pre != nullptr, wqv);
   // epilogue operands: rows co0 + 4 kq + g, column t0 + l16
   const unsigned eo = lcol ? 4u * (unsigned)((co0 + 4 * kq) * P + t0 + l16) : kBufOut;
   const __amdgpu_buffer_rsrc_t srs = uniform_rsrc(a.skip + (long long)b * C * P, cp * C);
@@ -145,8 +141,7 @@ bool flow_tail_supported(int C, int half) { return (C == 128 || C == 192) && 2 *
 void launch_flow_tail(const FlowTailArgs& a, int C, int B, hipStream_t s) {
   RVC_CHECK(flow_tail_supported(C, C / 2), "flow_tail: unsupported channel count");
   RVC_CHECK(a.P >= 1 && B >= 1 && a.xb >= (long long)(C / 2) * a.P, "flow_tail: invalid shape");
-  RVC_CHECK(a.ld_rs >= C && a.ld_post >= C / 2 && (!a.w_pre || (a.ld_pre >= C && a.h && a.b_pre)),
-            "flow_tail: invalid weight layout");
+  RVC_CHECK(a.w_rs && a.w_post && (!a.w_pre || (a.h && a.b_pre)), "flow_tail: missing weights");
   // 32-bit byte offsets within one batch item's [C][P] tensors
   RVC_CHECK(4.0 * C * a.P < 2147483648.0, "flow_tail: sequence too long for 32-bit offsets");
   const dim3 grid((unsigned)((a.P + BN - 1) / BN), (unsigned)B);

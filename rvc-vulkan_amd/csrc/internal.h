@@ -459,7 +459,7 @@ int launch_relpos_attention_partials(const float* qkv, const float* emb_k, const
 // enc_p's attention output block in one launch (attn_out.hip): merge of the
 // attention partials (KS > 1) or the merged output (KS == 1), conv_o + bias,
 // + the residual, LayerNorm over the C = H * D channels.  Tensors [B][C][P]
-// contiguous; w packed [C_in][ld] (w[ci * ld + co]).
+// contiguous; w in SessionBase::pack_mfma_lanes order.
 struct AttnOutArgs {
   const float* part;  // KS > 1
   const float* att;   // KS == 1
@@ -469,7 +469,7 @@ struct AttnOutArgs {
   const float* g;
   const float* beta;
   float* out;
-  int H, D, P, KS, ld;
+  int H, D, P, KS;
   float eps;
 };
 bool attn_out_ln_supported(int H, int D, int KS);
@@ -478,8 +478,8 @@ void launch_attn_out_ln(const AttnOutArgs& a, int B, hipStream_t s);
 // The end of a reverse flow and the next flow's pre conv in one launch
 // (flow_tail.hip): skip' = skip + (W_rs acts + b_rs); x1 -= W_post skip' +
 // b_post; h = W_pre x1 + b_pre (skipped when w_pre is null).  acts, skip, h
-// [B][C][P] contiguous; x1 [HALF = C / 2][P] at batch stride xb; weights
-// packed [C_in][ld] (w[ci * ld + co]).
+// [B][C][P] contiguous; x1 [HALF = C / 2][P] at batch stride xb; weights in
+// SessionBase::pack_mfma_lanes order.
 struct FlowTailArgs {
   const float* acts;
   const float* skip;
@@ -492,7 +492,7 @@ struct FlowTailArgs {
   const float* w_pre;
   const float* b_pre;
   float* h;
-  int P, ld_rs, ld_post, ld_pre;
+  int P;
 };
 bool flow_tail_supported(int C, int half);
 void launch_flow_tail(const FlowTailArgs& a, int C, int B, hipStream_t s);

@@ -95,6 +95,24 @@ struct SessionBase {
     return o;
   }
 
+  // [O][K] (a 1x1 conv) -> the A operands of v_mfma_f32_16x16x4_f32 in load
+  // order, for kernels that keep a 16-row block's weights in registers: block
+  // b (rows 16 b ..), step group j (k in [16 j, 16 j + 16)), lane l = 16 q + r
+  // holds float4 {W[16 b + r][16 j + 4 u + q], u = 0..3}, at
+  // ((b * (K / 16) + j) * 64 + l) * 4 + u.  A wave's load of group j is then
+  // 64 consecutive float4s.
+  static std::vector<float> pack_mfma_lanes(const std::vector<float>& w, long long O, long long K) {
+    RVC_CHECK(O % 16 == 0 && K % 16 == 0 && (long long)w.size() == O * K,
+              "pack_mfma_lanes: O and K must be multiples of 16");
+    std::vector<float> r(w.size());
+    for (long long b = 0; b < O / 16; ++b)
+      for (long long j = 0; j < K / 16; ++j)
+        for (long long l = 0; l < 64; ++l)
+          for (long long u = 0; u < 4; ++u)
+            r[((b * (K / 16) + j) * 64 + l) * 4 + u] = w[(16 * b + l % 16) * K + 16 * j + 4 * u + l / 16];
+    return r;
+  }
+
   // [C_out][C_in][K] -> bf16 [K][C_out][bf16_ld(C_in)], pad channels zero
   static std::vector<uint16_t> pack_bf16(const std::vector<float>& w, long long C_out, long long C_in, long long K) {
     const long long ld = bf16_ld((int)C_in);

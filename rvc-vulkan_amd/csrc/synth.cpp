@@ -47,6 +47,7 @@ struct Synth : SessionBase {
   float *emb_phone_w = nullptr, *emb_phone_b = nullptr, *emb_pitch = nullptr, *emb_g = nullptr;
   struct EncL {
     float *wqkv, *bqkv, *wo, *bo, *ek, *ev, *g1, *b1, *w1, *bf1, *w2, *bf2, *g2, *b2;
+    float* wo_lanes;  // conv_o in pack_mfma_lanes order (attn_out_ln_kernel), or null
     uint16_t *wqkv16, *wo16, *w116, *w216;  // bf16 copies (precision >= 1), else null
   };
   std::vector<EncL> enc;
@@ -61,6 +62,9 @@ struct Synth : SessionBase {
     float *pre_w, *pre_b, *post_w, *post_b;
     float *in_w[kWnLayers], *in_b[kWnLayers], *rs_w[kWnLayers], *rs_b[kWnLayers];
     int rs_out[kWnLayers];
+    // the flow tail's weights in pack_mfma_lanes order (null when H does not
+    // take the flow tail): the last res/skip conv, post, pre
+    float *rs_lanes, *post_lanes, *pre_lanes;
   };
   std::vector<FlowL> flows;
   // every flow's cond_layer stacked, [n_flows * 2H * kWnLayers][gin]
@@ -288,6 +292,7 @@ struct Synth : SessionBase {
       L.wo16 = upload_conv16(b16, a + ".conv_o", H, H, 1, false);
       L.bqkv = upload(bqkv);
       L.wo = upload_conv(a + ".conv_o", H, H, 1, false);
+      L.wo_lanes = H % 16 == 0 ? upload(pack_mfma_lanes(conv_host(a + ".conv_o", H, H, 1, false), H, H)) : nullptr;
       L.bo = upload_vec(a + ".conv_o.bias", H);
       check_shape(a + ".emb_rel_k", W(a + ".emb_rel_k").shape, {1, 2 * kWindow + 1, kc});
       check_shape(a + ".emb_rel_v", W(a + ".emb_rel_v").shape, {1, 2 * kWindow + 1, kc});
@@ -336,6 +341,10 @@ struct Synth : SessionBase {
       L.pre_w = upload(pack(pw, H, half, 1));
       L.pre_b = upload_vec(b + ".pre.bias", H);
       L.post_w = upload(pack(qw, half, H, 1));
+      if (flow_tail_supported(H, half)) {
+        L.pre_lanes = upload(pack_mfma_lanes(pw, H, half));
+        L.post_lanes = upload(pack_mfma_lanes(qw, half, H));
+      }
       L.post_b = upload(qb);
       const HostT& cv = W(b + ".enc.cond_layer.weight_v");
       check_shape(b + ".enc.cond_layer.weight_v", cv.shape, {GW, gin, 1});
@@ -352,6 +361,8 @@ struct Synth : SessionBase {
         L.rs_out[i] = i < kWnLayers - 1 ? 2 * H : H;
         L.rs_w[i] = upload_conv(rl, L.rs_out[i], H, 1, true);
         L.rs_b[i] = upload_vec(rl + ".bias", L.rs_out[i]);
+        if (i == kWnLayers - 1 && flow_tail_supported(H, half))
+          L.rs_lanes = upload(pack_mfma_lanes(conv_host(rl, L.rs_out[i], H, 1, true), H, H));
       }
       flows.push_back(L);
     }
@@ -534,7 +545,7 @@ struct Synth : SessionBase {
         AttnOutArgs ao{};
         ao.part = apart;
         ao.att = att;
-        ao.w = L.wo;
+        ao.w = L.wo_lanes;
         ao.bias = L.bo;
         ao.res = i == 0 ? xin : xo;
         ao.g = L.g1;
@@ -544,7 +555,6 @@ struct Synth : SessionBase {
         ao.D = kc;
         ao.P = P;
         ao.KS = KS;
-        ao.ld = packed_ld(H);
         ao.eps = 1e-5f;
         const double in_bytes = KS > 1 ? 4.0 * B * heads * KS * (kc + 2.0) * P : 4.0 * B * HP;
         run("enc.o", 2.0 * B * H * (double)H * P, in_bytes + 4.0 * (3.0 * B * HP + (double)H * H),
@@ -681,21 +691,18 @@ struct Synth : SessionBase {
         FlowTailArgs ta{};
         ta.acts = acts;
         ta.skip = skip;
-        ta.w_rs = L.rs_w[kl];
+        ta.w_rs = L.rs_lanes;
         ta.b_rs = L.rs_b[kl];
-        ta.ld_rs = packed_ld(L.rs_out[kl]);
-        ta.w_post = L.post_w;
+        ta.w_post = L.post_lanes;
         ta.b_post = L.post_b;
-        ta.ld_post = packed_ld(half);
         ta.x1 = x1;
         ta.xb = HP;
         ta.P = P;
         if (fi > 0) {
           const FlowL& N = flows[fi - 1];
           RVC_CHECK(N.rev != L.rev, "flow: the next flow must read the half this one updates");
-          ta.w_pre = N.pre_w;
+          ta.w_pre = N.pre_lanes;
           ta.b_pre = N.pre_b;
-          ta.ld_pre = packed_ld(H);
           ta.h = h;
         }
         const double nxt = fi > 0 ? (double)H * half : 0.0;
