@@ -424,15 +424,25 @@ __device__ __forceinline__ void persist_tile(int lin, int n_tx, int n_ty, int& t
 // floats of x (every thread's XPT values: the window of the widest halo) and
 // WREG4 float4 of weights (the largest tap count's block); each wave waits
 // for its own loads before the chunk's barrier.
-template <int BM, int BN, int WM, int WN, int BK, int FAM, bool DIRECT = false>
+//
+// HC > 0: the staged input window's row stride is XWC = BN + HC, HC (16 or
+// 64) at least the launch's largest halo (K - 1) dil, a compile-time
+// constant: the MFMA operands' LDS addresses are then immediate offsets from
+// one base per tap, and the staging offsets need no division by a runtime
+// width.  HC = 0: the stride is the item's own window, BN + (K - 1) dil
+// (fewer registers: the 32-row tiles, which measured faster this way).
+template <int BM, int BN, int WM, int WN, int BK, int FAM, bool DIRECT = false, int HC = 0>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(4)))
 void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floats, int cpx) {
   using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
   constexpr int NT = C::NT, TM = C::TM, TN = C::TN, BKT = BK;
-  constexpr int XPT = C::XPT, WPT = C::WPT, W4ROW = C::W4ROW;
+  constexpr int WPT = C::WPT, W4ROW = C::W4ROW;
   static_assert(BK % 4 == 0 && (BK / 2) % 2 == 0, "channel chunk must be a multiple of 4");
-  constexpr int XREG = XPT * NT;
+  static_assert(HC <= kConvHaloMax, "halo class");
+  constexpr int XWC = BN + (HC > 0 ? HC : kConvHaloMax);  // the widest staged row
+  constexpr int XPT = (BKT * XWC + NT - 1) / NT;
+  constexpr int XREG = HC > 0 ? (BKT * XWC + 63) / 64 * 64 : XPT * NT;  // whole waves of direct-to-LDS loads
   constexpr int WREG4 = kConvTapsMax * BKT * W4ROW;
   // the weight loads past WREG4 (the last round only) skip whole waves
   static_assert(!DIRECT || ((WPT - 1) * NT < WREG4 && WPT * NT >= WREG4 && (WREG4 - (WPT - 1) * NT) % 64 == 0),
@@ -500,15 +510,21 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     s_XW = BN + (s_K - 1) * s_dil;
     s_x = G.x + (long long)s_b * a.xb;
     s_w = G.w;
-    const int nx = BKT * s_XW;
     const int nw4 = s_K * BKT * W4ROW;
     const int tbase = s_i0 + G.in_off;
 #pragma unroll
     for (int e = 0; e < XPT; ++e) {
       const int idx = tid + e * NT;
-      const int row = idx / s_XW;
-      const int t = tbase + idx - row * s_XW;
-      xo[e] = idx < nx && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
+      if constexpr (HC > 0) {  // LDS row stride XWC, the item's window in its first s_XW columns
+        const int row = idx / XWC;
+        const int col = idx - row * XWC;
+        const int t = tbase + col;
+        xo[e] = row < BKT && col < s_XW && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
+      } else {  // LDS row stride s_XW
+        const int row = idx / s_XW;
+        const int t = tbase + idx - row * s_XW;
+        xo[e] = idx < BKT * s_XW && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
+      }
     }
 #pragma unroll
     for (int e = 0; e < WPT; ++e) {
@@ -535,7 +551,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(s_w + (long long)ci0 * a.w_ld, wr);
 #pragma unroll
     for (int e = 0; e < XPT; ++e) xv[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, xo[e], 0, 0));
-    float4* ws4 = reinterpret_cast<float4*>(smem + nb * stage_floats + BKT * s_XW);
+    float4* ws4 = reinterpret_cast<float4*>(smem + nb * stage_floats + BKT * (HC > 0 ? XWC : s_XW));
     const int nw4 = s_K * BKT * W4ROW;
     const int wb = wave * 64;
 #pragma unroll
@@ -551,7 +567,8 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     float4* ws4 = reinterpret_cast<float4*>(xs + XREG);
     const int wb = wave * 64;
 #pragma unroll
-    for (int e = 0; e < XPT; ++e) buffer_load_lds_b32(xrs, xs + e * NT + wb, xo[e]);
+    for (int e = 0; e < XPT; ++e)
+      if (HC == 0 || e + 1 < XPT || e * NT + wb < XREG) buffer_load_lds_b32(xrs, xs + e * NT + wb, xo[e]);
 #pragma unroll
     for (int e = 0; e < WPT; ++e)
       if (e + 1 < WPT || e * NT + wb < WREG4) buffer_load_lds_b128(wrs, ws4 + e * NT + wb, wo[e]);
@@ -560,11 +577,10 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   auto wait_loads = [&]() { __builtin_amdgcn_s_waitcnt(0); };
   auto lstore = [&](int buf) {
     float* xs = smem + buf * stage_floats;
-    const int nx = BKT * s_XW;
 #pragma unroll
     for (int e = 0; e < XPT; ++e) {
       const int idx = tid + e * NT;
-      if (idx < nx) {
+      if (idx < BKT * (HC > 0 ? XWC : s_XW)) {
         float v = xv[e];
         if (a.in_act == ACT_LEAKY) v = v >= 0.f ? v : v * a.in_slope;
         xs[idx] = v;
@@ -575,7 +591,8 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
   // MFMAs of one staged chunk (software-pipelined LDS operands, as in the
   // one-shot kernel)
   floatx16 acc[TM][TN];
-  auto mfma_chunk = [&](int buf, int K, int dil, int XW) {
+  auto mfma_chunk = [&](int buf, int K, int dil, int XWr) {
+    const int XW = HC > 0 ? XWC : XWr;  // the LDS row stride
     const float* xs = smem + buf * stage_floats;
     const float* ws = xs + (DIRECT ? XREG : BKT * XW);
     const float* wbase = ws + half * BM + wm * WM + l32;
@@ -1413,54 +1430,58 @@ bool persist_ok(const ConvLaunch& a) {
   return true;
 }
 
-template <int BM, int BN, int WM, int WN, int BK, bool DIRECT>
+template <int BM, int BN, int WM, int WN, int BK, bool DIRECT, int HC>
 bool launch_persist_kernel(const ConvLaunch& a, hipStream_t s, int stage, size_t lds, int n_tx, int n_ty, bool fam,
                            long long items) {
   using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
-  const void* kern = fam ? reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT>)
-                         : reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT>);
+  const void* k1 = reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT, HC>);
+  const void* k0 = reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT, HC>);
   // 64 KiB of staging plus the kernel's static ticket word: allow the
   // dynamic part its full size (a CU holds 160 KiB)
   if (lds > 65536 - 256) {
     static bool attr = false;  // per instantiation
     if (!attr) {
-      RVC_HIP(hipFuncSetAttribute(
-          reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit));
-      RVC_HIP(hipFuncSetAttribute(
-          reinterpret_cast<const void*>(&conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit));
+      RVC_HIP(hipFuncSetAttribute(k1, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit));
+      RVC_HIP(hipFuncSetAttribute(k0, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit));
       attr = true;
     }
   }
-  const int per_cu = resident_blocks(kern, C::NT, lds);
+  const int per_cu = resident_blocks(fam ? k1 : k0, C::NT, lds);
   if (per_cu < 1) return false;
   long long grid = (long long)per_cu * device_cus();
   if (grid >= 8) grid -= grid % 8;  // item j then runs on XCD j % 8
   grid = std::min(grid, items);
   const int cpx = device_cus() % 8 == 0 ? device_cus() / 8 : 0;  // CUs per XCD
   if (fam)
-    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT>), dim3((unsigned)grid), dim3(C::NT),
-                       lds, s, a, n_tx, n_ty, stage, cpx);
+    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT, HC>), dim3((unsigned)grid),
+                       dim3(C::NT), lds, s, a, n_tx, n_ty, stage, cpx);
   else
-    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT>), dim3((unsigned)grid), dim3(C::NT),
-                       lds, s, a, n_tx, n_ty, stage, cpx);
+    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT, HC>), dim3((unsigned)grid),
+                       dim3(C::NT), lds, s, a, n_tx, n_ty, stage, cpx);
   check_launch("conv1d_mfma_persist");
   return true;
 }
 
 template <int BM, int BN, int WM, int WN, int BK>
 bool launch_persist(const ConvLaunch& a, hipStream_t s) {
-  using C = Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>;
   if (a.C_out % BM != 0) return false;  // the epilogue has no row guard
   // inputs that take no activation are staged by direct-to-LDS loads
   const bool direct = a.in_act == ACT_NONE;
+  // halo class (64-row tiles; the 32-row tiles keep the item's own stride,
+  // HC = 0): the staged window's row stride BN + 16 when every group's halo
+  // (K - 1) dil fits 16 columns (the dilation-1 launches), else BN + 64
+  int halo = 0;
+  for (int g = 0; g < a.n_groups; ++g) halo = std::max(halo, (a.g[g].K - 1) * a.g[g].dil);
+  const int HC = BM < 64 ? 0 : halo <= 16 ? 16 : kConvHaloMax;
   int stage = 0;  // floats per staging buffer
   if (direct) {
-    stage = C::XPT * C::NT + kConvTapsMax * BK * BM;
+    const int XWC = BN + (HC > 0 ? HC : kConvHaloMax);
+    const int xreg = HC > 0 ? (BK * XWC + 63) / 64 * 64 : Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>::XPT *
+                                                              Cfg<BM, BN, WM, WN, BK, 1, 1, kConvTapsMax, 2>::NT;
+    stage = xreg + kConvTapsMax * BK * BM;
   } else {
     for (int g = 0; g < a.n_groups; ++g) {  // the largest group
-      const int XW = BN + (a.g[g].K - 1) * a.g[g].dil;
+      const int XW = HC > 0 ? BN + HC : BN + (a.g[g].K - 1) * a.g[g].dil;
       stage = std::max(stage, BK * XW + a.g[g].K * BK * BM);
     }
     stage = (stage + 3) / 4 * 4;  // keeps each buffer's weight block 16-byte aligned
@@ -1473,8 +1494,18 @@ bool launch_persist(const ConvLaunch& a, hipStream_t s) {
   RVC_CHECK(items < (1LL << 30), "conv1d_mfma: launch too large");
   bool fam = a.n_groups == 3;
   for (int g = 0; g < a.n_groups; ++g) fam = fam && a.g[g].combine == COMB_STORE;
-  return direct ? launch_persist_kernel<BM, BN, WM, WN, BK, true>(a, s, stage, lds, n_tx, n_ty, fam, items)
-                : launch_persist_kernel<BM, BN, WM, WN, BK, false>(a, s, stage, lds, n_tx, n_ty, fam, items);
+  if constexpr (BM < 64) {
+    return direct ? launch_persist_kernel<BM, BN, WM, WN, BK, true, 0>(a, s, stage, lds, n_tx, n_ty, fam, items)
+                  : launch_persist_kernel<BM, BN, WM, WN, BK, false, 0>(a, s, stage, lds, n_tx, n_ty, fam, items);
+  } else {
+    if (direct)
+      return HC == 16 ? launch_persist_kernel<BM, BN, WM, WN, BK, true, 16>(a, s, stage, lds, n_tx, n_ty, fam, items)
+                      : launch_persist_kernel<BM, BN, WM, WN, BK, true, kConvHaloMax>(a, s, stage, lds, n_tx, n_ty,
+                                                                                     fam, items);
+    return HC == 16 ? launch_persist_kernel<BM, BN, WM, WN, BK, false, 16>(a, s, stage, lds, n_tx, n_ty, fam, items)
+                    : launch_persist_kernel<BM, BN, WM, WN, BK, false, kConvHaloMax>(a, s, stage, lds, n_tx, n_ty,
+                                                                                    fam, items);
+  }
 }
 
 // Split-K plan for a single-group stride-1 launch whose output tiles alone
