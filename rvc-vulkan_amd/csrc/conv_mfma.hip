@@ -43,6 +43,7 @@
 #include <atomic>
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 #include "internal.h"
 
@@ -512,18 +513,31 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     s_w = G.w;
     const int nw4 = s_K * BKT * W4ROW;
     const int tbase = s_i0 + G.in_off;
+    if constexpr (HC > 0) {  // LDS row stride XWC, the item's window in its first s_XW columns
 #pragma unroll
-    for (int e = 0; e < XPT; ++e) {
-      const int idx = tid + e * NT;
-      if constexpr (HC > 0) {  // LDS row stride XWC, the item's window in its first s_XW columns
+      for (int e = 0; e < XPT; ++e) {
+        const int idx = tid + e * NT;
         const int row = idx / XWC;
         const int col = idx - row * XWC;
         const int t = tbase + col;
         xo[e] = row < BKT && col < s_XW && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
-      } else {  // LDS row stride s_XW
-        const int row = idx / s_XW;
-        const int t = tbase + idx - row * s_XW;
-        xo[e] = idx < BKT * s_XW && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
+      }
+    } else {
+      // LDS row stride s_XW: element idx = tid + e NT sits at row idx / s_XW,
+      // column idx % s_XW.  NT <= BN <= s_XW, so element 0 is (0, tid) and each
+      // step adds NT to the column, wrapping into the next row at most once:
+      // no division by the runtime width.
+      static_assert(HC > 0 || NT <= BN, "incremental staging offsets need NT <= BN");
+      int row = 0, col = tid;
+#pragma unroll
+      for (int e = 0; e < XPT; ++e) {
+        const int t = tbase + col;
+        xo[e] = row < BKT && t >= 0 && t < a.L_in ? 4u * (unsigned)(row * (int)a.xc + t) : kOut;
+        col += NT;
+        if (col >= s_XW) {
+          col -= s_XW;
+          ++row;
+        }
       }
     }
 #pragma unroll
@@ -734,23 +748,47 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     buf ^= 1;
 
     // ---- epilogue: ((acc + bias) [+ res]) -> act -> [pre +] -> store ----
+    // The bias goes through a buffer resource (range 0 without a bias: every
+    // load reads 0 and no lane branches), all its loads in flight together.
+    // The decoder's ResBlock launches (a bias, no activation, STORE, with or
+    // without a residual) take a path with those choices made once per item:
+    // two adds per value.
+    const bool hb = G.bias != nullptr;
+    const __amdgpu_buffer_rsrc_t brs = uniform_rsrc(G.bias, hb ? 4u * (unsigned)a.C_out : 0u);
+    auto epilogue = [&](auto fast, auto fres) {
 #pragma unroll
-    for (int m = 0; m < TM; ++m) {
-      float bias[16];
+      for (int m = 0; m < TM; ++m) {
+        float bias[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) bias[r] = G.bias ? G.bias[co_l + m * 32 + (r & 3) + 8 * (r >> 2)] : 0.f;
+        for (int r = 0; r < 16; ++r)
+          bias[r] = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(brs, 4u * (unsigned)co_l, 4 * (m * 32 + (r & 3) + 8 * (r >> 2)), 0));
 #pragma unroll
-      for (int n = 0; n < TN; ++n)
+        for (int n = 0; n < TN; ++n)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int roff = m * 32 + (r & 3) + 8 * (r >> 2);
-          float v = acc[m][n][r];
-          if (G.bias) v = v + bias[r];
-          if (res) v = v + pre[m][n][r];
-          v = apply_act(v, a.out_act, a.out_slope);
-          if (add) v = pre[m][n][r] + v;
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), ors, ooff[n], 4 * roff * (int)a.oc, 0);
-        }
+          for (int r = 0; r < 16; ++r) {
+            const int roff = m * 32 + (r & 3) + 8 * (r >> 2);
+            float v = acc[m][n][r];
+            if constexpr (decltype(fast)::value) {
+              v = v + bias[r];
+              if constexpr (decltype(fres)::value) v = v + pre[m][n][r];
+            } else {
+              if (hb) v = v + bias[r];
+              if (res) v = v + pre[m][n][r];
+              v = apply_act(v, a.out_act, a.out_slope);
+              if (add) v = pre[m][n][r] + v;
+            }
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), ors, ooff[n], 4 * roff * (int)a.oc, 0);
+          }
+      }
+    };
+    if (hb && a.out_act == ACT_NONE && !add) {
+      if (res)
+        epilogue(std::true_type{}, std::true_type{});
+      else
+        epilogue(std::true_type{}, std::false_type{});
+    } else {
+      epilogue(std::false_type{}, std::false_type{});
     }
     item = next;
   }
