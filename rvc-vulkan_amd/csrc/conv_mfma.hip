@@ -750,12 +750,12 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     // ---- epilogue: ((acc + bias) [+ res]) -> act -> [pre +] -> store ----
     // The bias goes through a buffer resource (range 0 without a bias: every
     // load reads 0 and no lane branches), all its loads in flight together.
-    // The decoder's ResBlock launches (a bias, no activation, STORE, with or
-    // without a residual) take a path with those choices made once per item:
-    // two adds per value.
+    // The decoder's ResBlock launches (a bias, STORE, no activation or the
+    // leaky ReLU, with or without a residual) take a path with those choices
+    // made once per item: two adds, or an add and the leaky ReLU, per value.
     const bool hb = G.bias != nullptr;
     const __amdgpu_buffer_rsrc_t brs = uniform_rsrc(G.bias, hb ? 4u * (unsigned)a.C_out : 0u);
-    auto epilogue = [&](auto fast, auto fres) {
+    auto epilogue = [&](auto fast, auto fres, auto fleaky) {
 #pragma unroll
       for (int m = 0; m < TM; ++m) {
         float bias[16];
@@ -772,6 +772,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
             if constexpr (decltype(fast)::value) {
               v = v + bias[r];
               if constexpr (decltype(fres)::value) v = v + pre[m][n][r];
+              if constexpr (decltype(fleaky)::value) v = v >= 0.f ? v : v * a.out_slope;
             } else {
               if (hb) v = v + bias[r];
               if (res) v = v + pre[m][n][r];
@@ -782,13 +783,17 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
           }
       }
     };
-    if (hb && a.out_act == ACT_NONE && !add) {
+    using T = std::true_type;
+    using F = std::false_type;
+    if (hb && !add && a.out_act == ACT_NONE) {
       if (res)
-        epilogue(std::true_type{}, std::true_type{});
+        epilogue(T{}, T{}, F{});
       else
-        epilogue(std::true_type{}, std::false_type{});
+        epilogue(T{}, F{}, F{});
+    } else if (hb && !add && !res && a.out_act == ACT_LEAKY) {
+      epilogue(T{}, F{}, T{});
     } else {
-      epilogue(std::false_type{}, std::false_type{});
+      epilogue(F{}, F{}, F{});
     }
     item = next;
   }
