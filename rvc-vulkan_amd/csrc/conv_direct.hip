@@ -413,10 +413,10 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
     constexpr int NT = 256, CH = kPostCh;
     dim3 grid((a.n_out + 4 * NT - 1) / (4 * NT), a.B);
     switch (a.K) {
-      case 3: hipLaunchKernelGGL((conv_post_kernel<3, NT, CH>), grid, dim3(NT), 0, s, a); break;
-      case 5: hipLaunchKernelGGL((conv_post_kernel<5, NT, CH>), grid, dim3(NT), 0, s, a); break;
-      case 7: hipLaunchKernelGGL((conv_post_kernel<7, NT, CH>), grid, dim3(NT), 0, s, a); break;
-      default: hipLaunchKernelGGL((conv_post_kernel<9, NT, CH>), grid, dim3(NT), 0, s, a); break;
+      case 3: launch_timed(conv_post_kernel<3, NT, CH>, grid, dim3(NT), 0, s, a); break;
+      case 5: launch_timed(conv_post_kernel<5, NT, CH>, grid, dim3(NT), 0, s, a); break;
+      case 7: launch_timed(conv_post_kernel<7, NT, CH>, grid, dim3(NT), 0, s, a); break;
+      default: launch_timed(conv_post_kernel<9, NT, CH>, grid, dim3(NT), 0, s, a); break;
     }
   } else if (a.stride == 1 && (long long)(a.K - 1) * a.dil <= kRowHaloMax) {
     dim3 grid((a.n_out + kRowOut - 1) / kRowOut, a.C_out, a.B);

@@ -1503,11 +1503,11 @@ bool launch_persist_kernel(const ConvLaunch& a, hipStream_t s, int stage, size_t
   grid = std::min(grid, items);
   const int cpx = device_cus() % 8 == 0 ? device_cus() / 8 : 0;  // CUs per XCD
   if (fam)
-    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT, HC>), dim3((unsigned)grid),
-                       dim3(C::NT), lds, s, a, n_tx, n_ty, stage, cpx);
+    launch_timed(conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 1, DIRECT, HC>, dim3((unsigned)grid), dim3(C::NT), lds,
+                 s, a, n_tx, n_ty, stage, cpx);
   else
-    hipLaunchKernelGGL((conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT, HC>), dim3((unsigned)grid),
-                       dim3(C::NT), lds, s, a, n_tx, n_ty, stage, cpx);
+    launch_timed(conv1d_mfma_persist_kernel<BM, BN, WM, WN, BK, 0, DIRECT, HC>, dim3((unsigned)grid), dim3(C::NT), lds,
+                 s, a, n_tx, n_ty, stage, cpx);
   check_launch("conv1d_mfma_persist");
   return true;
 }

@@ -473,8 +473,7 @@ bool launch_one(const ConvTOsLaunch& a, hipStream_t s) {
   }
   const long long grid = (long long)a.B * (a.C_out / C::BM) * ((a.M + C::BN - 1) / C::BN);
   RVC_CHECK(grid < (1LL << 31), "convt_os: launch too large");
-  hipLaunchKernelGGL((convt_os_kernel<K, S, TM, TN, WMW, WNW, BK, FUSED, BF>), dim3((unsigned)grid), dim3(C::NT), lds,
-                     s, a);
+  launch_timed(convt_os_kernel<K, S, TM, TN, WMW, WNW, BK, FUSED, BF>, dim3((unsigned)grid), dim3(C::NT), lds, s, a);
   check_launch("convt_os");
   return true;
 }

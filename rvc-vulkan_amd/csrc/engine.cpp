@@ -37,6 +37,11 @@ void check_launch(const char* what) {
   if (e != hipSuccess) throw Error(std::string(what) + " launch failed: " + hipGetErrorString(e));
 }
 
+StopHook& stop_hook() {
+  static thread_local StopHook h;
+  return h;
+}
+
 Engine* engine_from_handle(long long h) {
   std::lock_guard<std::mutex> lk(g_tab_mu);
   auto it = g_engines.find(h);

@@ -6,6 +6,7 @@
 // are passed explicitly so kernels can read channel slices in place.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -39,6 +40,31 @@ void set_last_error(const std::string& msg);
   } while (0)
 
 void check_launch(const char* what);
+
+// Kernel-end events without a marker packet.  An event recorded between two
+// kernels is a marker the command processor runs between them, idling the
+// GPU for a few microseconds; a stop event attached to the kernel's own
+// dispatch (hipExtLaunchKernelGGL) costs nothing.  While a session times a
+// launch, stop_hook().ev is the end event of its timing span: the launch
+// sites that end their call's work with one kernel (the persistent conv,
+// the ConvTranspose and conv_post kernels) launch through launch_timed(),
+// which attaches it and counts the launch in `used`; the session records
+// the event itself when no launch did.
+struct StopHook {
+  hipEvent_t ev = nullptr;
+  int used = 0;
+};
+StopHook& stop_hook();  // this thread's
+template <typename F, typename... Args>
+inline void launch_timed(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+  StopHook& h = stop_hook();
+  if (h.ev) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, s, nullptr, h.ev, 0u, args...);
+    ++h.used;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+  }
+}
 
 // ---------------------------------------------------------------- conv args
 // Activation applied while loading an input tile (prologue) or before the

@@ -32,10 +32,13 @@ struct SessionBase {
   };
   // Consecutive timed launches on one stream share one event pair: an event
   // record between two kernels costs several microseconds of idle GPU, which
-  // would otherwise land inside the very region being timed.
+  // would otherwise land inside the very region being timed.  The end event
+  // b is attached to the span's kernels themselves where the launch site
+  // supports it (stop_hook()); b_done: the span's last launch did so.
   struct Span {
     bool open = false;
-    hipEvent_t a{};
+    hipEvent_t a{}, b{};
+    bool b_done = false;
     hipStream_t st{};
     double flops = 0, bytes = 0;
     long long n = 0;
@@ -50,7 +53,7 @@ struct SessionBase {
     if (eng && eng->stream) (void)hipStreamSynchronize(eng->stream);
     for (void* p : owned) (void)hipFree(p);
     for (auto& kv : ws) (void)hipFree(kv.second.first);
-    if (span.open) pool.push_back(span.a);
+    if (span.open) pool.push_back(span.a), pool.push_back(span.b);
     for (auto& e : pending) pool.push_back(e.a), pool.push_back(e.b);
     for (hipEvent_t e : pool) (void)hipEventDestroy(e);
   }
@@ -206,11 +209,15 @@ struct SessionBase {
       return;
     }
     if (!st) st = eng->stream;
+    struct Depth {  // also restored when fn throws
+      int& d;
+      explicit Depth(int& x) : d(x) { ++d; }
+      ~Depth() { --d; }
+    };
     if (!timed(t)) {
       close_span();
-      ++run_depth;
+      Depth dg(run_depth);
       fn();
-      --run_depth;
       return;
     }
     if (span.open && span.st != st) close_span();
@@ -218,12 +225,20 @@ struct SessionBase {
       span = Span{};
       span.open = true;
       span.a = ev();
+      span.b = ev();
       span.st = st;
       RVC_HIP(hipEventRecord(span.a, st));
     }
-    ++run_depth;
-    fn();
-    --run_depth;
+    {
+      Depth dg(run_depth);
+      struct Hook {  // the span's end event for launch_timed(), cleared also when fn throws
+        StopHook& h;
+        explicit Hook(StopHook& x, hipEvent_t e) : h(x) { h = StopHook{e, 0}; }
+        ~Hook() { h = StopHook{}; }
+      } hook(stop_hook(), span.b);
+      fn();
+      span.b_done = hook.h.used > 0;
+    }
     span.flops += flops;
     span.bytes += bytes;
     ++span.n;
@@ -233,9 +248,8 @@ struct SessionBase {
   void close_span() {
     if (!span.open) return;
     span.open = false;
-    hipEvent_t b = ev();
-    RVC_HIP(hipEventRecord(b, span.st));
-    pending.push_back(Ev{span.a, b, span.flops, span.bytes, span.n});
+    if (!span.b_done) RVC_HIP(hipEventRecord(span.b, span.st));
+    pending.push_back(Ev{span.a, span.b, span.flops, span.bytes, span.n});
   }
   void collect_timing() {
     // Only a call that ended early (an error) leaves a span open here; its
@@ -254,7 +268,7 @@ struct SessionBase {
     pending.clear();
   }
   void set_timing(const char* t) {
-    if (span.open) pool.push_back(span.a);
+    if (span.open) pool.push_back(span.a), pool.push_back(span.b);
     span.open = false;
     tag = t ? t : "";
     t_ms = t_flops = t_bytes = 0;
