@@ -229,6 +229,7 @@ struct SessionBase {
       span.st = st;
       RVC_HIP(hipEventRecord(span.a, st));
     }
+    span.b_done = false;  // until this launch attaches the end event (not if fn throws)
     {
       Depth dg(run_depth);
       struct Hook {  // the span's end event for launch_timed(), cleared also when fn throws
