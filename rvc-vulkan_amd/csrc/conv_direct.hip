@@ -405,7 +405,7 @@ void launch_conv1d_direct(const DirectConvArgs& a, hipStream_t s) {
   if (a.C_in == 1 && a.dil == 1 && !a.x2 && a.C_out >= 8 && a.stride <= 64 &&
       c1_lds_floats(a.K, a.stride) * sizeof(float) <= 65536) {
     dim3 grid((a.n_out + kC1Out - 1) / kC1Out, (a.C_out + kC1Co - 1) / kC1Co, a.B);
-    hipLaunchKernelGGL(conv1d_c1_kernel, grid, dim3(256), c1_lds_floats(a.K, a.stride) * sizeof(float), s, a);
+    launch_timed(conv1d_c1_kernel, grid, dim3(256), c1_lds_floats(a.K, a.stride) * sizeof(float), s, a);
   } else if (a.C_out >= 8) {
     dim3 grid((a.n_out + 255) / 256, (a.C_out + 7) / 8, a.B);
     hipLaunchKernelGGL(conv1d_direct_kernel<8>, grid, dim3(256), 0, s, a);

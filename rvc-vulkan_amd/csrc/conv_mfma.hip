@@ -1636,7 +1636,7 @@ void launch_small_conv_cfg(const ConvLaunch& a, dim3 grid, hipStream_t s) {
       attr = true;
     }
   }
-  hipLaunchKernelGGL((conv_small_kernel<BN, K, CHK, NW>), grid, dim3(NT), lds, s, a);
+  launch_timed(conv_small_kernel<BN, K, CHK, NW>, grid, dim3(NT), lds, s, a);
 }
 
 bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
@@ -1714,9 +1714,9 @@ bool launch_small_gemm(const ConvLaunch& a, hipStream_t s) {
     attr = true;
   }
   if (wide)
-    hipLaunchKernelGGL(conv1x1_small_kernel<64>, grid, dim3(256), lds, s, a);
+    launch_timed(conv1x1_small_kernel<64>, grid, dim3(256), lds, s, a);
   else
-    hipLaunchKernelGGL(conv1x1_small_kernel<32>, grid, dim3(256), lds, s, a);
+    launch_timed(conv1x1_small_kernel<32>, grid, dim3(256), lds, s, a);
   check_launch("conv1x1_small");
   return true;
 }

@@ -395,7 +395,7 @@ void launch_bias_add(float* out, const float* a, const float* bias, long long n,
 
 void launch_avg3(float* out, const float* a, const float* b, const float* c, long long n, hipStream_t s) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(avg3_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, b, c, n);
+  launch_timed(avg3_kernel, dim3(capped_grid(n)), dim3(256), 0, s, out, a, b, c, n);
   check_launch("avg3");
 }
 void launch_embed_i32(const int* ids, const float* table, float* out, long long n, int rows, int dim,

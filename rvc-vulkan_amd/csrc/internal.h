@@ -46,8 +46,9 @@ void check_launch(const char* what);
 // GPU for a few microseconds; a stop event attached to the kernel's own
 // dispatch (hipExtLaunchKernelGGL) costs nothing.  While a session times a
 // launch, stop_hook().ev is the end event of its timing span: the launch
-// sites that end their call's work with one kernel (the persistent conv,
-// the ConvTranspose and conv_post kernels) launch through launch_timed(),
+// sites that end their call's work with one kernel (the persistent, small
+// and 1x1 conv kernels, the ConvTranspose, conv_post, stage-0 noise conv and
+// ResBlock-average kernels) launch through launch_timed(),
 // which attaches it and counts the launch in `used`; the session records
 // the event itself when no launch did.
 struct StopHook {
