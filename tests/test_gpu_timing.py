@@ -52,8 +52,11 @@ def setup():
 
 
 # (tag, launches per call): 4 stages x 6 ResBlock launches; one conv_post;
-# four upsamplers; stage 1's six launches alone; enc_p (event-recorded ends)
-CASES = [("dec.rb", 24), ("dec.post", 1), ("dec.ups", 4), ("dec.rb.s1", 6), ("enc", None)]
+# four upsamplers; stage 1's six launches alone; the averages of stages 0-2
+# (stage 3's is folded into conv_post); conv_pre; enc_p and the flow (spans
+# of many launches, most ending with an event record)
+CASES = [("dec.rb", 24), ("dec.post", 1), ("dec.ups", 4), ("dec.rb.s1", 6), ("dec.avg", 3), ("dec.pre", 1),
+         ("enc", None), ("flow", None)]
 
 
 @pytest.mark.parametrize("tag,per_call", CASES)
