@@ -1651,10 +1651,13 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   // tile's operand reuse (config 2: flow 0.375 -> 0.360 ms, enc_p 0.725 ->
   // 0.709 ms against a threshold of 192).  The reduction order does not
   // depend on the tile width or the batch.
-  // The tall 1x1 GEMMs (C_out >= 2304: HuBERT's q/k/v and FFN input) stay on
-  // 32 columns: 1152 / 1536 workgroups instead of 576 / 768 even out the
-  // per-CU load (config 3 3400 -> 3490 audio-s/s, q/k/v 0.453 -> 0.391 ms).
-  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 320 && !(K == 1 && a.C_out >= 2304);
+  // The tall 1x1 GEMMs (C_out >= 2304: HuBERT's q/k/v and FFN input) and
+  // the short-reduction 3-tap convs (enc_p's FFN input, C_in 192) stay on 32
+  // columns: 1152 / 1536 / 768 workgroups instead of 576 / 768 / 384 even out
+  // the per-CU load (config 3 3400 -> 3490 audio-s/s, q/k/v 0.453 -> 0.391 ms;
+  // enc_p 0.63 -> 0.61 ms).
+  const bool wide = (long long)((n_out + 63) / 64) * nco * z >= 320 && !(K == 1 && a.C_out >= 2304) &&
+                    !(K == 3 && a.C_in < 512);
   const int BN = wide ? 64 : 32;
   // 128-channel chunks for the long 3-tap reductions (enc_p's FFN output
   // conv, C_in = 768): half the chunk round trips.  Never for a gated launch:
