@@ -884,7 +884,7 @@ __device__ __forceinline__ void ln_column_stats(const double* stat, int ntile, i
 template <int BN, int NW = 4>
 __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const ConvGroup& G, int b, int i0, int co0,
                                                     bool gate, const floatx16 (&acc)[BN / 32], float* red, float rs_mu,
-                                                    float rs_rd) {
+                                                    float rs_rd, int split = -1) {
   constexpr int TN = BN / 32;
   constexpr int RS = 64 * NW / BN;
   constexpr int KO = 32 * BN / (64 * NW);
@@ -921,6 +921,19 @@ __device__ __forceinline__ void small_conv_epilogue(const ConvLaunch& a, const C
     bo[k] = ok ? 4u * (unsigned)co : kOut;
     oo[k] = ok ? 4u * (unsigned)(co * (int)a.oc + i) : kOut;
     ro[k] = ok ? 4u * (unsigned)(co * (int)a.rc + i) : kOut;
+  }
+  if (split >= 0) {
+    // one split of a split reduction: the raw partial tile to
+    // part[split][b][C_out][n_out]; splitk_small_reduce_kernel forms the output
+    const long long pb = ((long long)split * a.B + b) * a.C_out * G.n_out;
+    const __amdgpu_buffer_rsrc_t prs = uniform_rsrc(a.part + pb, 4u * (unsigned)(a.C_out * G.n_out));
+#pragma unroll
+    for (int k = 0; k < KO; ++k) {
+      const int row = tid / BN + k * RS;
+      const unsigned po = icol && co0 + row < a.C_out ? 4u * (unsigned)((co0 + row) * G.n_out + i) : kOut;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[k]), prs, po, 0, 0);
+    }
+    return;
   }
   float bv[KO];
   if (G.bias) {
@@ -1219,8 +1232,14 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
   extern __shared__ float smem[];
   float* ws = smem;                // [K][CHK][32]
   float* xs = smem + K * CHK * 32; // [XE * NT] (CHK rows of XW, tail unused)
-  const int b = blockIdx.z % a.B;
-  const int gi = blockIdx.z / a.B;
+  // blockIdx.z = (split * n_groups + group) * B + batch item; sc_split > 1
+  // (1x1 launches only): this workgroup reduces over chunks [c_lo, c_hi) of
+  // the input channels and stores a raw partial tile
+  const int nsplit = a.sc_split > 1 ? a.sc_split : 1;
+  const int zb = blockIdx.z % (a.B * a.n_groups);
+  const int sidx = blockIdx.z / (a.B * a.n_groups);
+  const int b = zb % a.B;
+  const int gi = zb / a.B;
   const ConvGroup& G = a.g[gi];
   const int i0 = blockIdx.x * BN;
   if (i0 >= G.n_out) return;  // uniform for the whole workgroup, before any barrier
@@ -1234,6 +1253,7 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
   const int l32 = lane & 31;
   const int C_in = a.C_in;
   const int n_ch = C_in / CHK;
+  const int c_lo = sidx * (n_ch / nsplit), c_hi = c_lo + n_ch / nsplit;  // the launcher requires n_ch % nsplit == 0
 
   const __amdgpu_buffer_rsrc_t wrs = uniform_rsrc(G.w, 4u * (unsigned)(K * C_in * a.w_ld));
   const __amdgpu_buffer_rsrc_t xrs =
@@ -1280,7 +1300,7 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
   constexpr int Q = CHK / NW;
   const float* wl = ws + (wave * Q + half) * 32 + l32;
   const float* xl = xs + (wave * Q + half) * XW + l32;
-  load(0);
+  load(c_lo);
   // LayerNorms from the producers' column statistics (1x1 launches only;
   // a thread stages and finishes one column, tid % BN): of the input while
   // it is staged (no affine: the caller folds gamma / beta into the weights
@@ -1292,10 +1312,10 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
   float ln_mu = 0.f, ln_rd = 0.f, rs_mu = 0.f, rs_rd = 0.f;
   if constexpr (kLn) {
     if (ln) ln_column_stats<NT, BN>(a.ln_stat, a.ln_ntile, C_in, a.L_in, a.ln_eps, b, i0, xs, ln_mu, ln_rd);
-    if (a.res_stat)
+    if (a.res_stat && nsplit == 1)
       ln_column_stats<NT, BN>(a.res_stat, a.C_out / 32, a.C_out, G.n_out, a.ln_eps, b, i0, xs, rs_mu, rs_rd);
   }
-  for (int c = 0; c < n_ch; ++c) {
+  for (int c = c_lo; c < c_hi; ++c) {
 #pragma unroll
     for (int j = 0; j < WF4; ++j) reinterpret_cast<float4*>(ws)[j * NT + tid] = wv[j];
     if (ln) {
@@ -1310,7 +1330,7 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
       }
     }
     __syncthreads();
-    if (c + 1 < n_ch) load(c + 1);
+    if (c + 1 < c_hi) load(c + 1);
 #pragma unroll 2
     for (int st = 0; st < Q / 2; ++st) {
       float av[K], bv[K][TN];
@@ -1325,9 +1345,91 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
 #pragma unroll
         for (int n = 0; n < TN; ++n) acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[k], bv[k][n], acc[n], 0, 0, 0);
     }
-    if (c + 1 < n_ch) __syncthreads();  // the next chunk's stores overwrite this one
+    if (c + 1 < c_hi) __syncthreads();  // the next chunk's stores overwrite this one
   }
-  small_conv_epilogue<BN, NW>(a, G, b, i0, co0, gate, acc, smem, rs_mu, rs_rd);
+  small_conv_epilogue<BN, NW>(a, G, b, i0, co0, gate, acc, smem, rs_mu, rs_rd, nsplit > 1 ? sidx : -1);
+}
+
+// The output of a split chunked 1x1 launch (sc_split > 1): for output column
+// i of 32-row tile blockIdx.y, out = ((sum_s part[s]) + bias) + res, the
+// splits added in index order and the residual normalised from a.res_stat
+// when set (the small-conv epilogue's formulas); with a.stat_out, the float64
+// (sum, sum of squares) of the tile's stored values per column.  A workgroup
+// takes 64 columns x the tile's 32 rows, thread (g, c) rows 8g .. 8g + 7 of
+// column c, every operand loaded before the first store; the statistics are
+// added per thread in row order, then over g in order.
+__global__ __launch_bounds__(256) void splitk_small_reduce_kernel(ConvLaunch a) {
+  const ConvGroup& G = a.g[0];
+  const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int i = blockIdx.x * 64 + c;
+  const int tile = blockIdx.y, b = blockIdx.z;
+  const bool icol = i < G.n_out;
+  const int S = a.sc_split, ntile = a.C_out / 32;
+  __shared__ double red[4][64][2];
+  float mu = 0.f, rd = 0.f;
+  if (a.res_stat && icol) {
+    const double2* st = reinterpret_cast<const double2*>(a.res_stat) + (long long)b * ntile * G.n_out + i;
+    double sm = 0.0, sq = 0.0;
+    for (int t = 0; t < ntile; ++t) {
+      const double2 w = st[(long long)t * G.n_out];
+      sm += w.x;
+      sq += w.y;
+    }
+    const double md = sm / a.C_out;
+    mu = (float)md;
+    rd = 1.0f / sqrtf((float)(fmax(sq - sm * md, 0.0) / a.C_out) + a.ln_eps);
+  }
+  constexpr unsigned kOut = 0x80000000u;
+  const int r0 = tile * 32 + 8 * rg;  // this thread's first row
+  const unsigned plane = 4u * (unsigned)(a.B * a.C_out * G.n_out);  // bytes of one split's partials
+  const __amdgpu_buffer_rsrc_t prs = uniform_rsrc(a.part, plane * (unsigned)S);
+  const unsigned po = icol ? 4u * (unsigned)(((long long)b * a.C_out + r0) * G.n_out + i) : kOut;
+  const bool hr = G.res != nullptr;
+  const __amdgpu_buffer_rsrc_t rrs =
+      uniform_rsrc(hr ? G.res + (long long)b * a.rb : G.out, hr ? 4u * (unsigned)(a.C_out * (int)a.rc) : 0u);
+  const unsigned ro = icol ? 4u * (unsigned)(r0 * (int)a.rc + i) : kOut;
+  float v[8], rv[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    v[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, po, 4 * r * G.n_out, 0));
+    rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rrs, ro, 4 * r * (int)a.rc, 0));
+  }
+  for (int u = 1; u < S; ++u) {
+    const unsigned pu = icol ? po + u * plane : kOut;
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      v[r] = v[r] + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, pu, 4 * r * G.n_out, 0));
+  }
+  double sm = 0.0, sq = 0.0;
+  if (icol) {
+    float* op = G.out + (long long)b * a.ob + (long long)r0 * a.oc + i;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int co = r0 + r;
+      float t = v[r];
+      if (G.bias) t = t + G.bias[co];
+      if (hr) {
+        float x = rv[r];
+        if (a.res_stat) x = (x - mu) * rd * a.res_g[co] + a.res_b[co];
+        t = t + x;
+      }
+      op[(long long)r * a.oc] = t;
+      sm += t;
+      sq += (double)t * t;
+    }
+  }
+  if (!a.stat_out) return;  // uniform: no barrier follows
+  red[rg][c][0] = sm;
+  red[rg][c][1] = sq;
+  __syncthreads();
+  if (rg == 0 && icol) {
+    double tsm = red[0][c][0], tsq = red[0][c][1];
+    for (int g = 1; g < 4; ++g) {
+      tsm += red[g][c][0];
+      tsq += red[g][c][1];
+    }
+    reinterpret_cast<double2*>(a.stat_out)[((long long)b * ntile + tile) * G.n_out + i] = make_double2(tsm, tsq);
+  }
 }
 
 // out = combine(act(sum_s part[s] + bias (+ bias2) (+ res))), the splits
@@ -1615,6 +1717,21 @@ bool small_conv_ok(const ConvLaunch& a) {
   return n_blocks(a, 64, 128) < 384;
 }
 
+// The reduction split of a chunked 1x1 launch, a function of the shape only
+// (so a batch and its items take the same summation order): the long
+// reductions (C_in >= 3072: HuBERT's FFN output GEMM, 384 workgroups of 24
+// chunks at 499 frames) run as two splits (768 workgroups of 12 chunks, three
+// per CU), their raw partial tiles through part, and
+// splitk_small_reduce_kernel forms the output.  Plain epilogues only: bias,
+// a residual (LayerNorm'ed from statistics or not), column statistics out.
+int small_conv_split(const ConvLaunch& a) {
+  if (a.n_groups != 1 || a.g[0].K != 1 || a.C_in < 3072 || a.C_in % 256 != 0 || a.C_out % 32 != 0) return 1;
+  if (a.post != POST_NONE || a.out_act != ACT_NONE || a.in_act != ACT_NONE || a.bias2 || a.ln_stat || a.ln_g)
+    return 1;
+  if (a.g[0].combine != COMB_STORE || a.g[0].in_step > 1 || small_gemm_ok(a) || !small_conv_ok(a)) return 1;
+  return 2;
+}
+
 template <int BN, int K, int CHK, int NW>
 void launch_small_conv_cfg(const ConvLaunch& a, dim3 grid, hipStream_t s) {
   constexpr int NT = 64 * NW;
@@ -1675,6 +1792,19 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
   // shape only, never of B or the tile width (which depends on B): the wave
   // count sets the summation order.
   if (K == 1) {
+    const int ss = small_conv_split(a);
+    if (ss > 1 && a.part && a.part_floats >= (size_t)ss * a.B * a.C_out * n_out &&
+        4.0 * ss * a.B * a.C_out * n_out < 2147483648.0) {
+      ConvLaunch sa = a;
+      sa.sc_split = ss;
+      const dim3 gs(grid.x, grid.y, grid.z * (unsigned)ss);
+      wide ? launch_small_conv_cfg<64, 1, 128, 8>(sa, gs, s) : launch_small_conv_cfg<32, 1, 128, 8>(sa, gs, s);
+      check_launch("conv_small");
+      launch_timed(splitk_small_reduce_kernel, dim3((unsigned)((n_out + 63) / 64), (unsigned)(a.C_out / 32), (unsigned)a.B),
+                   dim3(256), 0, s, sa);
+      check_launch("conv_small reduce");
+      return true;
+    }
     wide ? launch_small_conv_cfg<64, 1, 128, 8>(a, grid, s) : launch_small_conv_cfg<32, 1, 128, 8>(a, grid, s);
   } else if (K == 3) {
     if (CHK == 128)
@@ -1795,6 +1925,8 @@ bool conv1d_mfma_fuses_gate(const ConvLaunch& a) {
 }
 
 size_t conv1d_mfma_split_floats(const ConvLaunch& a) {
+  const int ss = small_conv_split(a);
+  if (ss > 1) return (size_t)ss * a.B * a.C_out * a.g[0].n_out;
   const SplitPlan p = split_plan(a);
   return p.S > 1 ? (size_t)p.S * a.B * a.C_out * a.g[0].n_out : 0;
 }

@@ -184,6 +184,10 @@ struct ConvLaunch {
   float* part;
   size_t part_floats;
   int ksplit, csplit;  // set by the launcher
+  // the chunked 1x1 small-conv kernel's reduction split over sc_split
+  // workgroups (set by the launcher; the partial tiles go to part, a reduce
+  // launch forms the output)
+  int sc_split;
   // what the split-K reduce (or the small-conv kernel) does with v = sum of
   // the splits + bias (the launch must take one of those paths:
   // conv1d_mfma_fuses_gate(a) for the gate):
