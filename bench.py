@@ -196,7 +196,10 @@ def bench_hubert(args):
     n = max(fam["launches"], 1)
     avg_s = fam["ms"] / 1e3 / n
     achieved = fam["flops"] / n / avg_s / 1e12 if avg_s > 0 else 0.0
-    roofline = {"kernel": "conv1d_mfma (HuBERT FFN 1x1 convs 768->3072->768)", "bound": "mfma",
+    # the FFN family: per layer the input GEMM and the output GEMM's two
+    # C_in halves plus their ordered reduce (three launches)
+    roofline = {"kernel": "conv_small (HuBERT FFN 1x1 GEMMs 768->3072->768, output GEMM split-K + reduce)",
+                "bound": "mfma",
                 "achieved": round(achieved, 2), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
                 "avg_launch_us": round(avg_s * 1e6, 2), "launches_per_step": n // args.steps,
