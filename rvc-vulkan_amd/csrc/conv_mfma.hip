@@ -1355,17 +1355,19 @@ __global__ __launch_bounds__(64 * NW) void conv_small_kernel(ConvLaunch a) {
 // splits added in index order and the residual normalised from a.res_stat
 // when set (the small-conv epilogue's formulas); with a.stat_out, the float64
 // (sum, sum of squares) of the tile's stored values per column.  A workgroup
-// takes 64 columns x the tile's 32 rows, thread (g, c) rows 8g .. 8g + 7 of
-// column c, every operand loaded before the first store; the statistics are
-// added per thread in row order, then over g in order.
+// takes kSrCols columns x the tile's 32 rows, thread (g, c) rows kSrRows * g
+// .. + kSrRows - 1 of column c, every operand loaded before the first store;
+// the statistics are added per thread in row order, then over g in order.
+constexpr int kSrCols = 32, kSrRows = 4, kSrGroups = 256 / kSrCols;  // 384 workgroups at 499 frames
+static_assert(kSrGroups * kSrRows == 32, "a workgroup covers the 32 rows of its tile");
 __global__ __launch_bounds__(256) void splitk_small_reduce_kernel(ConvLaunch a) {
   const ConvGroup& G = a.g[0];
-  const int c = threadIdx.x & 63, rg = threadIdx.x >> 6;
-  const int i = blockIdx.x * 64 + c;
+  const int c = threadIdx.x % kSrCols, rg = threadIdx.x / kSrCols;
+  const int i = blockIdx.x * kSrCols + c;
   const int tile = blockIdx.y, b = blockIdx.z;
   const bool icol = i < G.n_out;
   const int S = a.sc_split, ntile = a.C_out / 32;
-  __shared__ double red[4][64][2];
+  __shared__ double red[kSrGroups][kSrCols][2];
   float mu = 0.f, rd = 0.f;
   if (a.res_stat && icol) {
     const double2* st = reinterpret_cast<const double2*>(a.res_stat) + (long long)b * ntile * G.n_out + i;
@@ -1380,7 +1382,7 @@ __global__ __launch_bounds__(256) void splitk_small_reduce_kernel(ConvLaunch a) 
     rd = 1.0f / sqrtf((float)(fmax(sq - sm * md, 0.0) / a.C_out) + a.ln_eps);
   }
   constexpr unsigned kOut = 0x80000000u;
-  const int r0 = tile * 32 + 8 * rg;  // this thread's first row
+  const int r0 = tile * 32 + kSrRows * rg;  // this thread's first row
   const unsigned plane = 4u * (unsigned)(a.B * a.C_out * G.n_out);  // bytes of one split's partials
   const __amdgpu_buffer_rsrc_t prs = uniform_rsrc(a.part, plane * (unsigned)S);
   const unsigned po = icol ? 4u * (unsigned)(((long long)b * a.C_out + r0) * G.n_out + i) : kOut;
@@ -1388,23 +1390,23 @@ __global__ __launch_bounds__(256) void splitk_small_reduce_kernel(ConvLaunch a) 
   const __amdgpu_buffer_rsrc_t rrs =
       uniform_rsrc(hr ? G.res + (long long)b * a.rb : G.out, hr ? 4u * (unsigned)(a.C_out * (int)a.rc) : 0u);
   const unsigned ro = icol ? 4u * (unsigned)(r0 * (int)a.rc + i) : kOut;
-  float v[8], rv[8];
+  float v[kSrRows], rv[kSrRows];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
+  for (int r = 0; r < kSrRows; ++r) {
     v[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, po, 4 * r * G.n_out, 0));
     rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rrs, ro, 4 * r * (int)a.rc, 0));
   }
   for (int u = 1; u < S; ++u) {
     const unsigned pu = icol ? po + u * plane : kOut;
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
+    for (int r = 0; r < kSrRows; ++r)
       v[r] = v[r] + __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, pu, 4 * r * G.n_out, 0));
   }
   double sm = 0.0, sq = 0.0;
   if (icol) {
     float* op = G.out + (long long)b * a.ob + (long long)r0 * a.oc + i;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < kSrRows; ++r) {
       const int co = r0 + r;
       float t = v[r];
       if (G.bias) t = t + G.bias[co];
@@ -1424,7 +1426,7 @@ __global__ __launch_bounds__(256) void splitk_small_reduce_kernel(ConvLaunch a) 
   __syncthreads();
   if (rg == 0 && icol) {
     double tsm = red[0][c][0], tsq = red[0][c][1];
-    for (int g = 1; g < 4; ++g) {
+    for (int g = 1; g < kSrGroups; ++g) {
       tsm += red[g][c][0];
       tsq += red[g][c][1];
     }
@@ -1800,7 +1802,7 @@ bool launch_small_conv(const ConvLaunch& a, hipStream_t s) {
       const dim3 gs(grid.x, grid.y, grid.z * (unsigned)ss);
       wide ? launch_small_conv_cfg<64, 1, 128, 8>(sa, gs, s) : launch_small_conv_cfg<32, 1, 128, 8>(sa, gs, s);
       check_launch("conv_small");
-      launch_timed(splitk_small_reduce_kernel, dim3((unsigned)((n_out + 63) / 64), (unsigned)(a.C_out / 32), (unsigned)a.B),
+      launch_timed(splitk_small_reduce_kernel, dim3((unsigned)((n_out + kSrCols - 1) / kSrCols), (unsigned)(a.C_out / 32), (unsigned)a.B),
                    dim3(256), 0, s, sa);
       check_launch("conv_small reduce");
       return true;
