@@ -2031,11 +2031,17 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   const bool persist = persist_ok(a);
   if (a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 900)
     ok = (persist && launch_persist<64, 256, 32, 64, 8>(a, s)) || launch_cfg<64, 256, 32, 64, 8, 1>(a, s);
+  // The persistent 64 x 256 tile down to 300 tiles (decoder stage 0, C = 256:
+  // 480 tiles at 40k / P = 1000, 348 at 48k / P = 600), against 32 x 256
+  // tiles on twice the items: each input window is staged for 64 output rows
+  // instead of 32.  Stage 0 1.50-1.52 -> 1.42-1.44 ms (config 2 1108-1112 ->
+  // 1116-1119 audio-s/s), config 4 1097 -> 1115-1119 audio-s/s.
+  if (!ok && persist && a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 300) ok = launch_persist<64, 256, 32, 64, 8>(a, s);
   if (!ok && a.C_out <= 32 && n_blocks(a, 32, 512) >= 900)
     ok = (persist && launch_persist<32, 512, 32, 64, 8>(a, s)) || launch_cfg<32, 512, 32, 64, 8, 1>(a, s);
-  // wide channels with shorter grids (decoder stage 0): four-wave 32 x 256
-  // persistent tiles (measured 94 vs 91 TFLOP/s for the 64 x 128 one-shot
-  // tile on the C = 256 ResBlock launches)
+  // shorter grids still (stage 0 of short chunks, under 300 tiles of 64 x
+  // 256): four-wave 32 x 256 persistent tiles, twice the items (measured 94
+  // vs 91 TFLOP/s for the 64 x 128 one-shot tile on C = 256 ResBlock launches)
   if (!ok && persist && a.C_out % 32 == 0 && n_blocks(a, 32, 256) >= 900)
     ok = launch_persist<32, 256, 32, 64, 8>(a, s);
   if (!ok && a.C_out % 128 == 0 && n_blocks(a, 128, 128) >= 900) ok = launch_cfg<128, 128, 64, 64, 8, 1>(a, s);
