@@ -2031,12 +2031,22 @@ void launch_conv1d_mfma(const ConvLaunch& a, hipStream_t s) {
   const bool persist = persist_ok(a);
   if (a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 900)
     ok = (persist && launch_persist<64, 256, 32, 64, 8>(a, s)) || launch_cfg<64, 256, 32, 64, 8, 1>(a, s);
-  // The persistent 64 x 256 tile down to 300 tiles (decoder stage 0, C = 256:
-  // 480 tiles at 40k / P = 1000, 348 at 48k / P = 600), against 32 x 256
-  // tiles on twice the items: each input window is staged for 64 output rows
-  // instead of 32.  Stage 0 1.50-1.52 -> 1.42-1.44 ms (config 2 1108-1112 ->
-  // 1116-1119 audio-s/s), config 4 1097 -> 1115-1119 audio-s/s.
-  if (!ok && persist && a.C_out % 64 == 0 && n_blocks(a, 64, 256) >= 300) ok = launch_persist<64, 256, 32, 64, 8>(a, s);
+  // The persistent 64 x 256 tile also where its 300 .. 2 x CUs tiles per
+  // batch item fit one round of its slots (two per CU; decoder stage 0, C =
+  // 256: 480 tiles at 40k / P = 1000, 348 at 48k / P = 600): each input window
+  // is staged for 64 output rows instead of 32.  Against the 32 x 256
+  // persistent tile (P = 1000) stage 0 went 1.50-1.52 -> 1.42-1.44 ms, config
+  // 2 1108-1112 -> 1116-1119 audio-s/s; against the one-shot 64 x 128 tile
+  // that takes stage 0 below 900 32 x 256 tiles, config 4 (B = 8) 1097 ->
+  // 1115-1119 audio-s/s, but a single P = 700 call 6.98 -> 7.10 ms (336 items
+  // fill two thirds of the slots).  The choice may not depend on B (the
+  // one-shot tile sums in another order), so the window follows the benchmark
+  // shapes.  Between one and two rounds the 32 x 256 items balance better
+  // (P = 380: stages 1-2 with 891-894 tiles, 4.30 against 4.60 ms per call).
+  if (!ok && persist && a.C_out % 64 == 0) {
+    const long long nb = n_blocks(a, 64, 256);
+    if (nb >= 300 && nb <= 2LL * device_cus()) ok = launch_persist<64, 256, 32, 64, 8>(a, s);
+  }
   if (!ok && a.C_out <= 32 && n_blocks(a, 32, 512) >= 900)
     ok = (persist && launch_persist<32, 512, 32, 64, 8>(a, s)) || launch_cfg<32, 512, 32, 64, 8, 1>(a, s);
   // shorter grids still (stage 0 of short chunks, under 300 tiles of 64 x
