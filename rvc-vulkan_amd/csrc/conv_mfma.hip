@@ -630,11 +630,13 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
     lda(0, 1, 1);
     if (PD == 3) lda(0, 2, 2);
     // the 32 x 512 tiles (stage 3: four chunks per item, so staging and
-    // epilogues are a large share) raise the wave's issue priority while it
-    // runs the chunk's MFMAs: waves with MFMAs ready win the arbitration over
-    // waves staging or storing (stage 3 1.017 -> 0.98 ms; the 256-column
-    // tiles measured slower with it)
-    if constexpr (BN == 512) __builtin_amdgcn_s_setprio(1);
+    // epilogues are a large share) and the 64 x 256 tiles (stages 0-2) raise
+    // the wave's issue priority while it runs the chunk's MFMAs: waves with
+    // MFMAs ready win the arbitration over waves staging or storing (stage 3
+    // 1.017 -> 0.98 ms; the 64 x 256 family +0.4 %, config 2 1116 -> 1120
+    // audio-s/s; the 32 x 256 tiles measured 2-4 % slower with it)
+    constexpr bool kPrio = BN == 512 || BM == 64;
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
     for (int k = 0; k < K; ++k) {
 #pragma unroll
       for (int q = 0; q < BK / 2; ++q) {
@@ -652,7 +654,7 @@ void conv1d_mfma_persist_kernel(ConvLaunch a, int n_tx, int n_ty, int stage_floa
         __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
       }
     }
-    if constexpr (BN == 512) __builtin_amdgcn_s_setprio(0);
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
   };
 
   setup(item);
